@@ -1,0 +1,235 @@
+"""Benchmark: one GPU's share of the PlaceMoE expert layer, forward + backward.
+
+A step is one pass of the hot path over one batch of synthetic input:
+route (M table, histogram, scan, stable scatter index) -> permute -> fc1 +
+SwiGLU -> fc2 -> weighted combine, then the backward (combine gradient, fc2
+dgrad + SwiGLU backward, fc2 and fc1 wgrad, fc1 dgrad, unpermute gradient).
+Inputs and weights are resident in HBM before the timed region starts.
+
+Default workload: BASELINE config 2 (Qwen3-30B-A3B shape: T=16384, H=2048,
+E=128 -> C=160 copies, top-8, I=768, 8 sources).  ``--config`` picks another.
+
+Prints ONE JSON line.  ``value`` is the layer fwd+bwd time in ms (lower is
+better); the grouped-GEMM TFLOP/s and permute GB/s of the same run, the
+roofline of the dominant kernel (HIP-event durations on the kernels' stream)
+and a CPU baseline (the oracle on a bounded token sample, on the host cores)
+ride along.
+"""
+
+from __future__ import annotations
+
+import argparse
+import contextlib
+import json
+import os
+import sys
+import time
+from collections import defaultdict
+
+import numpy as np
+import torch
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
+
+# Entry-point call order inside one step; repeated names are told apart by
+# their occurrence index.
+STAGES = [
+    ("pmx_route", 0, "route"),
+    ("pmx_moe_scatter", 0, "permute"),
+    ("pmx_gemm_fc1_swiglu_fwd", 0, "fc1_fwd"),
+    ("pmx_group_gemm_nt", 0, "fc2_fwd"),
+    ("pmx_combine_fwd", 0, "combine_fwd"),
+    ("pmx_combine_bwd", 0, "combine_bwd"),
+    ("pmx_gemm_fc2_dgrad_swiglu_bwd", 0, "fc2_dgrad"),
+    ("pmx_group_gemm_tn", 0, "fc2_wgrad"),
+    ("pmx_group_gemm_tn", 1, "fc1_wgrad"),
+    ("pmx_group_gemm_nn", 0, "fc1_dgrad"),
+    ("pmx_moe_gather", 0, "unpermute_grad"),
+]
+
+
+class EventTimer:
+    """Brackets every C-ABI call with HIP events on torch's current stream (the
+    stream the kernels are launched on)."""
+
+    def __init__(self):
+        self.records = []
+        self._seen = defaultdict(int)
+
+    def new_step(self):
+        self._seen.clear()
+
+    @contextlib.contextmanager
+    def __call__(self, name):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        idx = self._seen[name]
+        self._seen[name] += 1
+        s.record()
+        yield
+        e.record()
+        self.records.append((name, idx, s, e))
+
+    def averages(self):
+        torch.cuda.synchronize()
+        acc = defaultdict(list)
+        for name, idx, s, e in self.records:
+            acc[(name, idx)].append(s.elapsed_time(e))
+        return {k: float(np.mean(v)) for k, v in acc.items()}
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--config", default="qwen3", choices=["toy", "qwen3", "dsv3", "skew", "fold"])
+    p.add_argument("--cpu-sample-tokens", type=int, default=1024)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--profile-steps", type=int, default=5, help="extra steps timed per kernel with HIP events")
+    return p.parse_args()
+
+
+def cpu_baseline(wl, sample_tokens: int, backward: bool):
+    """The CPU oracle (torch on the host cores) on the first ``sample_tokens``
+    tokens of the same workload, scaled linearly to the full token count."""
+    from oracle import moe_oracle as O
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    Ts = min(sample_tokens, wl.T)
+    x = wl.hidden[:Ts].cpu()
+    w = wl.routing_weights[:Ts].cpu()
+    sel = wl.selected[:Ts].cpu().numpy()
+    src = wl.sources[:Ts].cpu().numpy() if wl.sources is not None else np.zeros(Ts, dtype=np.int64)
+    M = wl.mapping.cpu().numpy()
+    fc1, fc2 = wl.fc1.cpu(), wl.fc2.cpu()
+    dout = torch.randn((Ts, wl.H), generator=torch.Generator().manual_seed(0)).to(torch.bfloat16)
+
+    def run():
+        phys = O.map_logical_to_physical(M, src, sel)
+        fwd = O.moe_layer_forward(x, w, phys, fc1, fc2)
+        if backward:
+            O.moe_layer_backward(dout, fwd, w, fc1, fc2)
+
+    run()  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    ms = float(np.median(times)) * 1e3
+    return {
+        "value": ms * wl.T / Ts,
+        "unit": "ms",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle layer {'fwd+bwd' if backward else 'fwd'} on {Ts} of {wl.T} tokens, median of 3 "
+                  f"({ms:.1f} ms), scaled x{wl.T / Ts:g} to the full batch",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(
+            json.dumps({"error": f"bench.py measures one GPU's share; --gpus {args.gpus} is not supported "
+                                 "(the multi-GPU exchange is outside this build)"}),
+            flush=True,
+        )
+        return 2
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import placemoe_amd  # noqa: F401
+    from placemoe_amd import _capi, experts
+    from placemoe_amd.workloads import algorithmic_work, make_workload
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = make_workload(args.config, device=dev)
+    backward = not wl.meta.get("forward_only", False)
+    T, K, H, I, C = wl.T, wl.K, wl.H, wl.I, wl.C
+    work = algorithmic_work(T, K, H, I, C)
+    x = wl.hidden.requires_grad_(backward)
+    w = wl.routing_weights.requires_grad_(backward)
+    fc1 = wl.fc1.requires_grad_(backward)
+    fc2 = wl.fc2.requires_grad_(backward)
+    dout = torch.randn((T, H), device=dev, generator=torch.Generator(device=dev).manual_seed(1)).to(torch.bfloat16)
+
+    def step():
+        for p in (x, w, fc1, fc2):
+            p.grad = None
+        out = experts.expert_layer(x, w, wl.selected, fc2, fc1_1_2_weight=fc1, mapping=wl.mapping,
+                                   sources=wl.sources)
+        if backward:
+            out.backward(dout)
+        return out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    timer = EventTimer()
+    _capi.set_timer(timer)
+    for _ in range(args.profile_steps):
+        timer.new_step()
+        step()
+    _capi.set_timer(None)
+    avg = timer.averages()
+    kernels_ms = {label: avg.get((name, idx)) for name, idx, label in STAGES if (name, idx) in avg}
+
+    flops = {"fc1_fwd": work["fc1_fwd_flops"], "fc2_fwd": work["fc2_fwd_flops"],
+             "fc2_dgrad": work["fc2_dgrad_flops"], "fc2_wgrad": work["fc2_wgrad_flops"],
+             "fc1_wgrad": work["fc1_wgrad_flops"], "fc1_dgrad": work["fc1_dgrad_flops"]}
+    gemm_ms = sum(kernels_ms[k] for k in flops if k in kernels_ms)
+    gemm_flops = sum(v for k, v in flops.items() if k in kernels_ms)
+    gemm_tflops = gemm_flops / (gemm_ms * 1e-3) / 1e12
+    dominant = max((k for k in flops if k in kernels_ms), key=lambda k: kernels_ms[k])
+    dom_tflops = flops[dominant] / (kernels_ms[dominant] * 1e-3) / 1e12
+    permute_gbps = work["permute_bytes"] / (kernels_ms["permute"] * 1e-3) / 1e9
+    bw = {"permute": work["permute_bytes"], "combine_fwd": work["combine_fwd_bytes"],
+          "combine_bwd": work["combine_bwd_bytes"], "unpermute_grad": work["unpermute_grad_bytes"],
+          "route": work["route_bytes"]}
+    bandwidth = {k: round(v / (kernels_ms[k] * 1e-3) / 1e9, 1) for k, v in bw.items() if k in kernels_ms}
+
+    result = {
+        "metric": "MoE layer fwd+bwd ms; grouped-GEMM TFLOP/s (%MFMA peak); permute GB/s",
+        "value": round(ms_per_step, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"config{['toy', 'qwen3', 'dsv3', 'skew', 'fold'].index(args.config) + 1}-"
+                               f"{args.config}", "tokens": T, "top_k": K, "hidden": H, "moe_intermediate": I,
+                   "physical_copies": C, "logical_experts": wl.num_experts, "seed": wl.seed,
+                   "pass": "fwd+bwd" if backward else "fwd"},
+        "gemm_tflops": round(gemm_tflops, 1),
+        "gemm_frac_mfma_peak": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+        "permute_gbps": round(permute_gbps, 1),
+        "permute_frac_hbm_peak": round(permute_gbps / PEAK_HBM_GBPS, 4),
+        "kernel_ms": {k: round(v, 4) for k, v in kernels_ms.items()},
+        "bandwidth_gbps": bandwidth,
+        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(dom_tflops, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_sample_tokens, backward)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

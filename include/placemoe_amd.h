@@ -1,0 +1,193 @@
+/*
+ * placemoe_amd.h - C ABI of the MI355X (gfx950) PlaceMoE expert-layer library.
+ *
+ * One GPU's share of the PlaceMoE / VeOmni MoE expert layer:
+ *   map (M table) -> histogram/scan -> permute -> SwiGLU grouped GEMM
+ *   (fwd, dgrad, wgrad) -> router-weighted combine -> replica-gradient fold.
+ *
+ * Conventions
+ *  - Every entry point returns PMX_OK (0) or a PMX_ERR_* code; nothing throws.
+ *  - All pointers are device pointers; every buffer, including workspace, is
+ *    allocated by the caller.  The library allocates nothing, never
+ *    synchronises the host, and enqueues work only on the given stream.
+ *  - bf16 tensors are passed as `const void*` holding bf16 bit patterns,
+ *    row-major and contiguous.  Index tensors are int32 unless stated.
+ *  - Each declaration names the reference (pia7a/PlaceMoE) interface it
+ *    replaces, as `file:line`.
+ */
+#ifndef PLACEMOE_AMD_H
+#define PLACEMOE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* pmx_stream_t; /* == hipStream_t */
+
+#define PMX_OK 0
+#define PMX_ERR_HIP 1      /* a HIP runtime call or kernel launch failed */
+#define PMX_ERR_ARG 2      /* bad argument: null pointer, negative size, K too large */
+#define PMX_ERR_SHAPE 3    /* shape the kernels do not support (e.g. dim not a multiple of 8) */
+#define PMX_ERR_RANGE 4    /* device check found an index outside its table (routing status word) */
+
+/* Library identification and error text. */
+const char* pmx_version(void);
+const char* pmx_error_string(int code);
+
+/* ------------------------------------------------------------------------ */
+/* Routing: map -> histogram -> scan -> stable scatter index                */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of workspace pmx_route needs for `num_assign` assignments over
+ * `num_slots` physical copies.  The first 16 bytes of the workspace hold the
+ * routing status word read by pmx_route_status. */
+size_t pmx_route_workspace_bytes(int64_t num_assign, int32_t num_slots);
+
+/* Full integer routing path, bit-exact with the reference:
+ *   phys[t,k]  = M[src[t], sel[t,k]]                (M table gather)
+ *   counts[c]  = #{(t,k) : phys[t,k] == c}           (histogram)
+ *   offsets[c] = sum_{c'<c} counts[c'], offsets[C] = T*K
+ *   pos[t,k]   = offsets[phys[t,k]] + #{a' < t*K+k : phys[a'] == phys[t,k]}
+ * i.e. pos = phys.flatten().argsort(stable=True).argsort().
+ * Replaces ExpertSwapManager.map_logical_to_physical
+ *   (veomni/distributed/moe/hiermoe/expert_swap.py:5831-5879, source LUT
+ *   gather at :5914-5921), expert_histogram
+ *   (veomni/ops/kernels/moe/_kernels/kernel/moe.py:53-82), the cumsum and
+ *   double argsort of MergedFc1TritonFusedMoeExpertFunction.forward
+ *   (veomni/ops/kernels/moe/group_gemm.py:473-477) and
+ *   _local_expert_sort_indices (veomni/distributed/moe/hiermoe/all_to_all.py:820-847).
+ * sel: int64 [T*K] logical expert ids.  M: int64 [S*E] (row s = source s), or
+ *   NULL for the identity map (phys = sel, then E must equal C).
+ * src: int64 [T] source ids, or NULL to use `src_const` for every token.
+ * Out-of-range ids are clamped and flagged in the status word. */
+int pmx_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t src_const,
+              int32_t S, int32_t E, int64_t T, int32_t K, int32_t C,
+              int32_t* phys, int32_t* counts, int32_t* offsets, int32_t* pos,
+              void* workspace, size_t workspace_bytes, pmx_stream_t stream);
+
+/* Copies the routing status word (0 = all indices valid) to host memory;
+ * synchronises `stream`.  For tests and debug validation only. */
+int pmx_route_status(const void* workspace, int32_t* status_host, pmx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Row movement                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* Xp[pos[t,k]] = X[t] for every k.  X [T,H] bf16 -> Xp [T*K,H] bf16.
+ * Replaces moe_scatter (veomni/ops/kernels/moe/_kernels/kernel/moe.py:299-333). */
+int pmx_moe_scatter(const void* X, const int32_t* pos, int64_t T, int32_t K, int64_t H,
+                    void* Xp, pmx_stream_t stream);
+
+/* out[t] = bf16( sum_k fp32(Y[pos[t,k]]) ).  Y [T*K,H] bf16 -> out [T,H] bf16.
+ * Replaces moe_gather (veomni/ops/kernels/moe/_kernels/kernel/moe.py:126-159). */
+int pmx_moe_gather(const void* Y, const int32_t* pos, int64_t T, int32_t K, int64_t H,
+                   void* out, pmx_stream_t stream);
+
+/* Router-weighted combine:
+ *   out[t] = bf16( sum_k fp32( bf16(Y[pos[t,k]] * w[t,k]) ) ),  w: bf16 [T,K].
+ * Replaces rank_dedup_combine (veomni/distributed/moe/hiermoe/all_to_all.py:2539-2564)
+ * with its fp32 segment sum (_aggregate_weighted_outputs :2266-2294,
+ * segment_sum_dim0_fp32_to_source_dtype triton_segment_sum.py:52-103) on one rank. */
+int pmx_combine_fwd(const void* Y, const int32_t* pos, const void* w, int64_t T, int32_t K,
+                    int64_t H, void* out, pmx_stream_t stream);
+
+/* Gradient of pmx_combine_fwd:
+ *   dY[pos[t,k]] = bf16(dout[t] * w[t,k])
+ *   dw[t,k]      = bf16( sum_h fp32( bf16(dout[t,h] * Y[pos[t,k],h]) ) )
+ * Replaces the autograd of the weighted multiply in rank_dedup_combine
+ * (all_to_all.py:2552) and _CudaIndexAddDim0CastOutput.backward (:930-933). */
+int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const void* w,
+                    int64_t T, int32_t K, int64_t H, void* dY, void* dw, pmx_stream_t stream);
+
+/* Bytes of workspace pmx_segment_sum needs. */
+size_t pmx_segment_sum_workspace_bytes(int64_t num_src_rows, int64_t num_rows);
+
+/* out[r] = sum_{i : index[i]==r} source[i] in fp32, stored as bf16.
+ * index: int64 [N]; rows are summed in ascending i (stable) order.
+ * Replaces segment_sum_dim0_fp32_to_source_dtype
+ * (veomni/distributed/moe/hiermoe/triton_segment_sum.py:52-103). */
+int pmx_segment_sum(const void* source, const int64_t* index, int64_t N, int64_t H,
+                    int64_t num_rows, void* out, void* workspace, size_t workspace_bytes,
+                    pmx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* SwiGLU grouped GEMM over per-copy row groups                              */
+/* ------------------------------------------------------------------------ */
+/* Group g owns rows [offsets[g], offsets[g+1]) of the permuted activations;
+ * offsets is the int32 [G+1] array produced by pmx_route (device memory).
+ * Weights of copy g: gate rows at w_gate + g*w_copy_stride, up rows at
+ * w_up + g*w_copy_stride, each [I, H] row-major.  A merged gate_up_proj
+ * [G, 2I, H] is w_gate = W, w_up = W + I*H, w_copy_stride = 2*I*H; split
+ * fc1_1/fc1_2 weights [G, I, H] use w_copy_stride = I*H.
+ * G <= 4096; H and I must be multiples of 8. */
+
+/* Forward fc1 with the SwiGLU epilogue:
+ *   gu[a, 0:I] = bf16(X[a] @ Wgate[g]^T), gu[a, I:2I] = bf16(X[a] @ Wup[g]^T)
+ *   act[a]     = bf16( bf16(silu(gate)) * up )
+ * X [A,H], gu [A,2I], act [A,I].  Replaces the fc1 group_gemm_same_nk +
+ * chunk + silu + multiply of EPMergedFc1GroupGemm.forward
+ * (veomni/distributed/moe/moe_layer.py:376-397) and EPGroupGemm.forward (:167-193). */
+int pmx_gemm_fc1_swiglu_fwd(const void* X, const void* w_gate, const void* w_up,
+                            int64_t w_copy_stride, const int32_t* offsets, int32_t G,
+                            int64_t A, int64_t H, int64_t I, void* gu, void* act,
+                            pmx_stream_t stream);
+
+/* Ragged-M grouped GEMM, B transposed: C[a] = bf16(A[a] @ B[g]^T), B [G,N,K].
+ * Forward fc2 (A = act, B = down_proj [G,H,I]).
+ * Replaces group_gemm_same_nk(transpose_b=True)
+ * (veomni/ops/kernels/moe/_kernels/kernel/group_gemm.py:170-247). */
+int pmx_group_gemm_nt(const void* A, const void* B, const int32_t* offsets, int32_t G,
+                      int64_t M, int64_t N, int64_t K, void* C, pmx_stream_t stream);
+
+/* Ragged-M grouped GEMM, B not transposed: C[a] = bf16(A[a] @ B[g]), B [G,K,N];
+ * B rows k >= b_split come from B1 (for split fc1 weights), else from B0;
+ * pass B1 = NULL for a single tensor.  dgrad fc1 (A = dG1 [A,2I]).
+ * Replaces group_gemm_same_nk(transpose_b=False) (group_gemm.py:170-247). */
+int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_copy_stride,
+                      int64_t b_split, const int32_t* offsets, int32_t G, int64_t M,
+                      int64_t N, int64_t K, void* C, pmx_stream_t stream);
+
+/* dgrad fc2 with the SwiGLU backward epilogue:
+ *   dact = bf16(dY[a] @ down[g])                      ([A,I])
+ *   dG1[a, 0:I] = d_gate, dG1[a, I:2I] = d_up         (silu_backward rounding)
+ * dY [A,H], down [G,H,I], gu [A,2I] from the forward, dG1 [A,2I].
+ * Replaces the dgrad + silu_backward + cat of EPMergedFc1GroupGemm.backward
+ * (veomni/distributed/moe/moe_layer.py:453-482). */
+int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void* gu,
+                                  const int32_t* offsets, int32_t G, int64_t A, int64_t H,
+                                  int64_t I, void* dG1, pmx_stream_t stream);
+
+/* Ragged-K grouped GEMM (weight gradient):
+ *   C[g] = bf16(A[rows of g]^T @ B[rows of g]),  A [rows,M], B [rows,N], C [G,M,N];
+ * a group with no rows stores zeros.  Rows m >= c_split of C[g] go to C1
+ * (split fc1 gradients), else to C0; pass C1 = NULL for one tensor.
+ * Replaces group_gemm_same_mn(transpose_a=True)
+ * (veomni/ops/kernels/moe/_kernels/kernel/group_gemm.py:370-410). */
+int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int32_t G,
+                      int64_t M, int64_t N, void* C0, void* C1, int64_t c_copy_stride,
+                      int64_t c_split, pmx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Replica-gradient fold                                                     */
+/* ------------------------------------------------------------------------ */
+
+/* out[e, p] = sum over copies c of e (copy_slots[copy_offsets[e] .. copy_offsets[e+1]),
+ *             slot order) with slot_tokens[c] > 0 of fp32(grads[c, p]).
+ * grads: bf16 [C,P]; out: fp32 [E,P]; slot_tokens: int64 [C] tokens seen by
+ * each copy, or NULL to treat every copy as active.  If writeback != 0 every
+ * copy of e (active or not) is overwritten with bf16(out[e]).
+ * Replaces _zero_inactive_slot_grads_for_layer (expert_swap.py:6250-6262),
+ * _replica_grad_contributions (:6839-6876) and _unpack_replica_grad
+ * (:6886-6889) for the copies held by one GPU. */
+int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const int32_t* copy_slots,
+                     const int64_t* slot_tokens, int32_t E, int32_t C, int64_t P, float* out,
+                     int32_t writeback, pmx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PLACEMOE_AMD_H */

@@ -1,0 +1,347 @@
+"""CPU oracle for the PlaceMoE expert-layer hot path (TEST INFRASTRUCTURE ONLY).
+
+This module restates, on the CPU, what the reference computes on the path
+map -> histogram/scan -> permute -> SwiGLU grouped GEMM (fwd, dgrad, wgrad)
+-> weighted combine -> replica-gradient fold.  It is the checker for the HIP
+library and nothing else: only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it.  The product path
+(``placemoe_amd``) never imports it and has no CPU fallback.
+
+Integer work is numpy; floating-point work is torch on the CPU in float32
+with bf16 rounding at the points where the reference stores bf16 tensors.
+
+Reference citations are paths under the reference repository
+(pia7a/PlaceMoE), ``file:line``.
+
+How each function is pinned (the checks live in ``tests/test_oracle_*.py``):
+
+* ``map_logical_to_physical`` - the reference's source-LUT known answer
+  (tests/distributed/test_hiermoe_forward_cover_planner.py:1032-1038), the
+  ``L[M] == e`` invariant and the mirrored-R2 closed form.
+* ``histogram`` / ``group_offsets`` - brute-force counting; sum == A.
+* ``scatter_index`` - a pure-Python stable insertion loop on small inputs,
+  and the permutation / stability invariants.
+* ``grouped_gemm_nt`` / ``grouped_gemm_nn`` / ``grouped_gemm_tn`` -
+  brute-force triple loops in float64 on tiny inputs.
+* ``expert_layer_forward`` / ``expert_layer_backward`` - an independent
+  float64 autograd model (the reference test's per-expert eager loop,
+  tests/ops/test_fused_moe_split_vs_merged.py:21-44), forward and gradients.
+* ``combine_forward`` / ``combine_backward`` / ``unpermute_grad`` - fp32
+  ``index_add_`` (tests/distributed/test_hiermoe_cuda_combine.py:41-51),
+  autograd of the weighted sum, and the reference's double-precision eager
+  linear MoE (tests/distributed/test_hiermoe.py:914-921).
+* ``replica_fold`` - the reference's known answer 10+2=12, 20+3=23
+  (tests/distributed/test_hiermoe.py:3286-3338) and "sum of copy grads ==
+  logical-expert grad of the eager model" (tests/distributed/test_hiermoe.py:3765-3778).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+BF16 = torch.bfloat16
+
+
+# ---------------------------------------------------------------------------
+# Integer routing path
+# ---------------------------------------------------------------------------
+
+
+def map_logical_to_physical(M: np.ndarray, src: np.ndarray, sel: np.ndarray) -> np.ndarray:
+    """phys[t, k] = M[src[t], sel[t, k]].
+
+    Follows ``ExpertSwapManager._map_logical_to_slot_dedup_aware``
+    (veomni/distributed/moe/hiermoe/expert_swap.py:5914-5921), which gathers row
+    ``ep_rank`` of ``source_logical_to_physical`` with ``index_select``.  Here the
+    source is per token (``src[t]``); the reference is the case ``src[:] = ep_rank``.
+    """
+    M = np.asarray(M, dtype=np.int64)
+    sel = np.asarray(sel, dtype=np.int64)
+    src = np.asarray(src, dtype=np.int64).reshape(-1)
+    if sel.ndim == 1:
+        sel = sel[:, None]
+    return M[src[:, None], sel]
+
+
+def histogram(phys: np.ndarray, num_bins: int) -> np.ndarray:
+    """counts[c] = #{(t,k) : phys[t,k] == c}.
+
+    ``expert_histogram`` (veomni/ops/kernels/moe/_kernels/kernel/moe.py:53-82) and
+    its EP analogue ``torch.bincount(..., minlength=C)``
+    (veomni/distributed/moe/hiermoe/all_to_all.py:827).
+    """
+    flat = np.asarray(phys, dtype=np.int64).reshape(-1)
+    if flat.size and (flat.min() < 0 or flat.max() >= num_bins):
+        raise ValueError("phys contains a slot outside [0, num_bins)")
+    return np.bincount(flat, minlength=num_bins).astype(np.int64)
+
+
+def group_offsets(counts: np.ndarray) -> np.ndarray:
+    """Exclusive prefix ``offsets[C+1]``; ``offsets[1:]`` is the reference's
+    inclusive ``cumsum_M`` (veomni/ops/kernels/moe/group_gemm.py:239,477,770)."""
+    counts = np.asarray(counts, dtype=np.int64)
+    out = np.zeros(counts.size + 1, dtype=np.int64)
+    np.cumsum(counts, out=out[1:])
+    return out
+
+
+def scatter_index(phys: np.ndarray) -> np.ndarray:
+    """pos[t,k] = rank of flat index t*K+k in a stable sort of phys.
+
+    ``phys.flatten().argsort(stable=True).argsort()``
+    (veomni/ops/kernels/moe/group_gemm.py:474); equivalently
+    ``offsets[phys] + #{a' < a : phys[a'] == phys[a]}``.
+    """
+    phys = np.asarray(phys, dtype=np.int64)
+    flat = phys.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    pos = np.empty_like(order)
+    pos[order] = np.arange(flat.size, dtype=np.int64)
+    return pos.reshape(phys.shape)
+
+
+def permute(X: torch.Tensor, pos: np.ndarray) -> torch.Tensor:
+    """Xp[pos[t,k]] = X[t]  (``moe_scatter``, moe.py:251-333)."""
+    pos_t = torch.as_tensor(np.asarray(pos, dtype=np.int64))
+    T, K = pos_t.shape
+    out = torch.empty((T * K, X.shape[1]), dtype=X.dtype)
+    out[pos_t.reshape(-1)] = X.repeat_interleave(K, dim=0)
+    return out
+
+
+def route(M, src, sel, num_slots):
+    """Convenience: the full integer routing path -> (phys, counts, offsets, pos)."""
+    phys = map_logical_to_physical(M, src, sel)
+    counts = histogram(phys, num_slots)
+    offsets = group_offsets(counts)
+    pos = scatter_index(phys)
+    return phys, counts, offsets, pos
+
+
+# ---------------------------------------------------------------------------
+# Grouped GEMM (fp32 accumulate, bf16 store)
+# ---------------------------------------------------------------------------
+
+
+def _groups(offsets):
+    offsets = np.asarray(offsets, dtype=np.int64)
+    for g in range(offsets.size - 1):
+        yield g, int(offsets[g]), int(offsets[g + 1])
+
+
+def grouped_gemm_nt(a: torch.Tensor, b: torch.Tensor, offsets) -> torch.Tensor:
+    """C[rows of g] = A[rows of g] @ B[g]^T, B: [G, N, K].
+
+    ``group_gemm_same_nk(..., transpose_b=True)``
+    (veomni/ops/kernels/moe/_kernels/kernel/group_gemm.py:67-247): fp32
+    accumulation (``tl.dot`` into fp32), stored in the input dtype.
+    """
+    out = torch.zeros((a.shape[0], b.shape[1]), dtype=torch.float32)
+    af = a.float()
+    for g, s, e in _groups(offsets):
+        if e > s:
+            out[s:e] = af[s:e] @ b[g].float().t()
+    return out.to(a.dtype)
+
+
+def grouped_gemm_nn(a: torch.Tensor, b: torch.Tensor, offsets) -> torch.Tensor:
+    """C[rows of g] = A[rows of g] @ B[g], B: [G, K, N]  (``same_nk``, transpose_b=False)."""
+    out = torch.zeros((a.shape[0], b.shape[2]), dtype=torch.float32)
+    af = a.float()
+    for g, s, e in _groups(offsets):
+        if e > s:
+            out[s:e] = af[s:e] @ b[g].float()
+    return out.to(a.dtype)
+
+
+def grouped_gemm_tn(a: torch.Tensor, b: torch.Tensor, offsets, out_dtype=None) -> torch.Tensor:
+    """C[g] = A[rows of g]^T @ B[rows of g]; zeros for empty groups.
+
+    ``group_gemm_same_mn(..., transpose_a=True)`` (group_gemm.py:254-410); an
+    empty group stores zeros (group_gemm.py:336-350).
+    """
+    offsets = np.asarray(offsets, dtype=np.int64)
+    G = offsets.size - 1
+    out = torch.zeros((G, a.shape[1], b.shape[1]), dtype=torch.float32)
+    af, bf = a.float(), b.float()
+    for g, s, e in _groups(offsets):
+        if e > s:
+            out[g] = af[s:e].t() @ bf[s:e]
+    return out.to(out_dtype or a.dtype)
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU expert MLP over per-copy groups
+# ---------------------------------------------------------------------------
+
+
+def silu_f32(x: torch.Tensor) -> torch.Tensor:
+    return x / (1.0 + torch.exp(-x))
+
+
+def swiglu_forward(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """act = bf16(bf16(silu(gate)) * up) - the two bf16 ops of
+    veomni/distributed/moe/moe_layer.py:394-397 (``aten.silu`` then ``*``)."""
+    s = silu_f32(gate.float()).to(BF16)
+    return (s.float() * up.float()).to(BF16)
+
+
+def swiglu_backward(dact: torch.Tensor, gate: torch.Tensor, up: torch.Tensor):
+    """Returns (d_gate, d_up) with the reference's bf16 rounding points
+    (veomni/distributed/moe/moe_layer.py:465-482)."""
+    g = gate.float()
+    s = silu_f32(g).to(BF16).float()
+    d_up = (s * dact.float()).to(BF16)
+    d_silu = (dact.float() * up.float()).to(BF16).float()
+    sig = torch.sigmoid(g)
+    d_gate = (d_silu * (sig * (1.0 + g * (1.0 - sig)))).to(BF16)
+    return d_gate, d_up
+
+
+def expert_layer_forward(xp: torch.Tensor, offsets, w1: torch.Tensor, w2: torch.Tensor):
+    """``EPMergedFc1GroupGemm.forward`` (veomni/distributed/moe/moe_layer.py:358-429).
+
+    xp [A,H] bf16, w1 = gate_up [C,2I,H], w2 = down [C,H,I].
+    Returns (gate_up [A,2I], act [A,I], y [A,H]).
+    """
+    gu = grouped_gemm_nt(xp, w1, offsets)
+    I = w1.shape[1] // 2
+    act = swiglu_forward(gu[:, :I], gu[:, I:])
+    y = grouped_gemm_nt(act, w2, offsets)
+    return gu, act, y
+
+
+def expert_layer_backward(dy, xp, gu, offsets, w1, w2):
+    """``EPMergedFc1GroupGemm.backward`` (veomni/distributed/moe/moe_layer.py:431-547).
+
+    Returns (dxp [A,H], dw1 [C,2I,H], dw2 [C,H,I], dg1 [A,2I]).
+    """
+    I = w1.shape[1] // 2
+    act = swiglu_forward(gu[:, :I], gu[:, I:])
+    dact = grouped_gemm_nn(dy, w2, offsets)
+    dw2 = grouped_gemm_tn(dy, act, offsets)
+    d_gate, d_up = swiglu_backward(dact, gu[:, :I], gu[:, I:])
+    dg1 = torch.cat([d_gate, d_up], dim=1)
+    dxp = grouped_gemm_nn(dg1, w1, offsets)
+    dw1 = grouped_gemm_tn(dg1, xp, offsets)
+    return dxp, dw1, dw2, dg1
+
+
+# ---------------------------------------------------------------------------
+# Combine (EP semantics) and its gradients
+# ---------------------------------------------------------------------------
+
+
+def combine_forward(y: torch.Tensor, pos, w: torch.Tensor) -> torch.Tensor:
+    """out[t] = bf16( sum_k fp32( bf16(y[pos[t,k]] * w[t,k]) ) ).
+
+    ``rank_dedup_combine`` (veomni/distributed/moe/hiermoe/all_to_all.py:2539-2564):
+    bf16 product with the router weight, then the fp32 segment sum of
+    ``_aggregate_weighted_outputs`` (:2266-2294) /
+    ``segment_sum_dim0_fp32_to_source_dtype``
+    (veomni/distributed/moe/hiermoe/triton_segment_sum.py:52-103).
+    """
+    pos_t = torch.as_tensor(np.asarray(pos, dtype=np.int64))
+    T, K = pos_t.shape
+    acc = torch.zeros((T, y.shape[1]), dtype=torch.float32)
+    for k in range(K):
+        rows = y[pos_t[:, k]].float()
+        acc += (rows * w[:, k : k + 1].float()).to(BF16).float()
+    return acc.to(y.dtype)
+
+
+def combine_backward(dout: torch.Tensor, y: torch.Tensor, pos, w: torch.Tensor):
+    """Gradients of ``combine_forward``: dy[pos[t,k]] = bf16(dout[t] * w[t,k]) and
+    dw[t,k] = bf16( sum_h fp32( bf16(dout[t,h] * y[pos[t,k],h]) ) ).
+
+    Autograd of the bf16 multiply in ``rank_dedup_combine`` (all_to_all.py:2552)
+    and the exact ``index_select`` backward of the segment sum (all_to_all.py:930-933).
+    """
+    pos_t = torch.as_tensor(np.asarray(pos, dtype=np.int64))
+    T, K = pos_t.shape
+    dy = torch.empty_like(y)
+    dw = torch.empty((T, K), dtype=w.dtype)
+    d = dout.float()
+    for k in range(K):
+        rows = y[pos_t[:, k]].float()
+        dy[pos_t[:, k]] = (d * w[:, k : k + 1].float()).to(y.dtype)
+        dw[:, k] = (d * rows).to(BF16).float().sum(dim=1).to(w.dtype)
+    return dy, dw
+
+
+def unpermute_grad(dxp: torch.Tensor, pos) -> torch.Tensor:
+    """dx[t] = bf16( sum_k fp32(dxp[pos[t,k]]) )  (``moe_gather``, moe.py:85-159)."""
+    pos_t = torch.as_tensor(np.asarray(pos, dtype=np.int64))
+    T, K = pos_t.shape
+    acc = torch.zeros((T, dxp.shape[1]), dtype=torch.float32)
+    for k in range(K):
+        acc += dxp[pos_t[:, k]].float()
+    return acc.to(dxp.dtype)
+
+
+def segment_sum(source: torch.Tensor, index, num_rows: int) -> torch.Tensor:
+    """out[r] = sum_{i: index[i]==r} source[i] in fp32, stored in source dtype
+    (triton_segment_sum.py:52-103)."""
+    index_t = torch.as_tensor(np.asarray(index, dtype=np.int64))
+    if index_t.numel() and (int(index_t.min()) < 0 or int(index_t.max()) >= num_rows):
+        raise ValueError("index contains a row outside [0, num_rows).")
+    out = torch.zeros((num_rows, source.shape[1]), dtype=torch.float32)
+    out.index_add_(0, index_t, source.float())
+    return out.to(source.dtype)
+
+
+# ---------------------------------------------------------------------------
+# Replica-gradient fold
+# ---------------------------------------------------------------------------
+
+
+def copy_groups(slot_to_logical, num_experts):
+    """Copies of each logical expert in slot order (``redundant_copy_groups``,
+    expert_swap.py:552-572; ``copy_slots_for_device`` :520-550)."""
+    L = np.asarray(slot_to_logical, dtype=np.int64)
+    return [[int(c) for c in np.nonzero(L == e)[0]] for e in range(num_experts)]
+
+
+def replica_fold(grads: torch.Tensor, slot_to_logical, num_experts: int, slot_counts=None) -> torch.Tensor:
+    """dW_logical[e] = sum_{c : L[c]==e} dW[c] in fp32.
+
+    ``_replica_grad_contributions`` (expert_swap.py:6839-6876) sums the copies of
+    each expert; slots with no accumulated tokens are zeroed first
+    (``_zero_inactive_slot_grads_for_layer``, expert_swap.py:6250-6262).  The sum
+    here is in fp32 (the reference sums in the gradient dtype).
+    """
+    C = grads.shape[0]
+    flat = grads.reshape(C, -1).float()
+    active = np.ones(C, dtype=bool) if slot_counts is None else (np.asarray(slot_counts) > 0)
+    out = torch.zeros((num_experts, flat.shape[1]), dtype=torch.float32)
+    for e, slots in enumerate(copy_groups(slot_to_logical, num_experts)):
+        for c in slots:
+            if active[c]:
+                out[e] += flat[c]
+    return out.reshape((num_experts,) + tuple(grads.shape[1:]))
+
+
+# ---------------------------------------------------------------------------
+# Whole layer (one GPU's share)
+# ---------------------------------------------------------------------------
+
+
+def moe_layer_forward(x, w, phys, w1, w2):
+    """Forward of the full path for already-mapped ``phys``; returns a dict of
+    every intermediate the backward needs."""
+    C = w1.shape[0]
+    counts = histogram(phys, C)
+    offsets = group_offsets(counts)
+    pos = scatter_index(phys)
+    xp = permute(x, pos)
+    gu, act, y = expert_layer_forward(xp, offsets, w1, w2)
+    out = combine_forward(y, pos, w)
+    return dict(counts=counts, offsets=offsets, pos=pos, xp=xp, gu=gu, act=act, y=y, out=out)
+
+
+def moe_layer_backward(dout, fwd, w, w1, w2):
+    dy, dw = combine_backward(dout, fwd["y"], fwd["pos"], w)
+    dxp, dw1, dw2, dg1 = expert_layer_backward(dy, fwd["xp"], fwd["gu"], fwd["offsets"], w1, w2)
+    dx = unpermute_grad(dxp, fwd["pos"])
+    return dict(dy=dy, dw=dw, dxp=dxp, dw1=dw1, dw2=dw2, dg1=dg1, dx=dx)

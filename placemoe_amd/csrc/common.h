@@ -1,0 +1,63 @@
+// Shared helpers for the gfx950 kernels of the PlaceMoE expert-layer path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/placemoe_amd.h"
+
+#define PMX_WAVE 64
+
+typedef uint16_t bf16_t;  // bf16 bit pattern in memory
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// bf16 -> fp32 is exact: the bf16 bits are the top half of the fp32 word.
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Unpack / pack 8 bf16 held in a uint4 (element 2j in the low half of word j).
+__device__ __forceinline__ void unpack8(const uint4 v, float* f) {
+  f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xffff0000u);
+  f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xffff0000u);
+  f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xffff0000u);
+  f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint4 v;
+  v.x = f32_to_bf16(f[0]) | (f32_to_bf16(f[1]) << 16);
+  v.y = f32_to_bf16(f[2]) | (f32_to_bf16(f[3]) << 16);
+  v.z = f32_to_bf16(f[4]) | (f32_to_bf16(f[5]) << 16);
+  v.w = f32_to_bf16(f[6]) | (f32_to_bf16(f[7]) << 16);
+  return v;
+}
+
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// Wave-wide sum (64 lanes) with cross-lane shuffles.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, PMX_WAVE);
+  return v;
+}
+
+static inline int pmx_status(hipError_t e) { return e == hipSuccess ? PMX_OK : PMX_ERR_HIP; }
+
+#define PMX_LAUNCH_CHECK()                         \
+  do {                                             \
+    hipError_t _e = hipGetLastError();             \
+    if (_e != hipSuccess) return PMX_ERR_HIP;      \
+  } while (0)

@@ -1,0 +1,578 @@
+// Integer routing path (map -> histogram -> scan -> stable rank) and the
+// bandwidth kernels that move rows (scatter, gather, weighted combine and
+// its gradient, segment sum) for gfx950.
+//
+// Stable ranks are computed without atomics on the ordering: the flat
+// assignment array is cut into chunks, one wave per chunk; a chunk's
+// histogram row gives, after a column-wise exclusive scan, the first output
+// position of every copy inside that chunk, and the wave then walks its chunk
+// in 64-element segments, ranking equal values with wave ballots
+// (match-any over the value bits) so that pos is identical to a stable
+// argsort.
+
+#include "common.h"
+
+#include <string.h>
+
+namespace {
+
+constexpr int kRouteLdsMaxSlots = 8192;  // LDS counters up to this many copies
+constexpr int kRouteMaxSlots = 1 << 24;
+constexpr int kMaxTopK = 32;
+
+struct RouteGeom {
+  int64_t chunk;    // assignments per chunk (multiple of 64)
+  int64_t nchunks;  // number of chunks (>= 1)
+};
+
+RouteGeom route_geom(int64_t A) {
+  RouteGeom g;
+  g.chunk = 2048;
+  g.nchunks = (A + g.chunk - 1) / g.chunk;
+  if (g.nchunks > 256) {
+    int64_t per = (A + 255) / 256;
+    g.chunk = (per + 63) / 64 * 64;
+    g.nchunks = (A + g.chunk - 1) / g.chunk;
+  }
+  if (g.nchunks < 1) g.nchunks = 1;
+  return g;
+}
+
+constexpr size_t kStatusBytes = 256;
+
+size_t route_ws_bytes(int64_t A, int32_t C) {
+  RouteGeom g = route_geom(A);
+  return kStatusBytes + (size_t)g.nchunks * (size_t)C * sizeof(int32_t);
+}
+
+__global__ void route_status_clear_kernel(int32_t* status) {
+  if (threadIdx.x == 0) status[0] = 0;
+}
+
+// Device-side fill (kept off hipMemsetAsync so the path can sit in a graph).
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// One wave per chunk: phys = M[src, sel] (clamped, flagged) and the chunk
+// histogram.  USE_LDS keeps the histogram in LDS, else in the chunk's own
+// row of the global table (chunk-private, so plain atomics are exact).
+template <bool USE_LDS>
+__global__ __launch_bounds__(64) void route_hist_kernel(
+    const int64_t* __restrict__ sel, const int64_t* __restrict__ M, const int64_t* __restrict__ src,
+    int32_t src_const, int32_t S, int32_t E, int32_t K, int32_t C, int64_t A, int64_t chunk,
+    int32_t* __restrict__ phys, int32_t* __restrict__ table, int32_t* __restrict__ status) {
+  extern __shared__ int32_t lds_hist[];
+  const int lane = threadIdx.x;
+  const int64_t ch = blockIdx.x;
+  int32_t* row = table + ch * (int64_t)C;
+  int32_t* hist = USE_LDS ? lds_hist : row;
+  for (int c = lane; c < C; c += 64) hist[c] = 0;
+  __syncthreads();
+  const int64_t begin = ch * chunk;
+  const int64_t end = begin + chunk < A ? begin + chunk : A;
+  int bad = 0;
+  for (int64_t a = begin + lane; a < end; a += 64) {
+    int64_t e = sel[a];
+    int64_t c;
+    if (M != nullptr) {
+      int64_t s = src != nullptr ? src[a / K] : (int64_t)src_const;
+      if (s < 0 || s >= S) { bad = 1; s = s < 0 ? 0 : S - 1; }
+      if (e < 0 || e >= E) { bad = 1; e = e < 0 ? 0 : E - 1; }
+      c = M[s * E + e];
+    } else {
+      c = e;
+    }
+    if (c < 0 || c >= C) { bad = 1; c = c < 0 ? 0 : C - 1; }
+    phys[a] = (int32_t)c;
+    atomicAdd(&hist[c], 1);
+  }
+  __syncthreads();
+  if (USE_LDS) {
+    for (int c = lane; c < C; c += 64) row[c] = hist[c];
+  }
+  if (bad) atomicOr(status, 1);
+}
+
+// Single block: column-wise exclusive scan of the chunk table (turning
+// histogram rows into per-chunk start positions), counts and offsets.
+__global__ __launch_bounds__(1024) void route_scan_kernel(int32_t* __restrict__ table, int64_t nchunks,
+                                                          int32_t C, int32_t* __restrict__ counts,
+                                                          int32_t* __restrict__ offsets) {
+  __shared__ int32_t sums[1024];
+  __shared__ int32_t carry_sh;
+  const int tid = threadIdx.x;
+  for (int c = tid; c < C; c += 1024) {
+    int32_t run = 0;
+    int64_t r = 0;
+    for (; r + 8 <= nchunks; r += 8) {
+      int32_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = table[(r + j) * C + c];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { table[(r + j) * C + c] = run; run += v[j]; }
+    }
+    for (; r < nchunks; ++r) {
+      int32_t v = table[r * C + c];
+      table[r * C + c] = run;
+      run += v;
+    }
+    counts[c] = run;
+  }
+  __syncthreads();
+  if (tid == 0) carry_sh = 0;
+  __syncthreads();
+  for (int base = 0; base < C; base += 1024) {
+    const int c = base + tid;
+    const int32_t v = c < C ? counts[c] : 0;
+    sums[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      int32_t add = tid >= off ? sums[tid - off] : 0;
+      __syncthreads();
+      sums[tid] += add;
+      __syncthreads();
+    }
+    const int32_t carry = carry_sh;
+    if (c < C) offsets[c] = carry + sums[tid] - v;
+    __syncthreads();
+    if (tid == 1023) carry_sh = carry + sums[1023];
+    __syncthreads();
+  }
+  if (tid == 0) offsets[C] = carry_sh;
+  __syncthreads();
+  for (int c = tid; c < C; c += 1024) {
+    const int32_t o = offsets[c];
+    for (int64_t r = 0; r < nchunks; ++r) table[r * C + c] += o;
+  }
+}
+
+// One wave per chunk: stable rank of every assignment among equal copies.
+template <bool USE_LDS>
+__global__ __launch_bounds__(64) void route_rank_kernel(const int32_t* __restrict__ phys,
+                                                         int32_t* __restrict__ table, int32_t C,
+                                                         int64_t A, int64_t chunk, int nbits,
+                                                         int32_t* __restrict__ pos) {
+  extern __shared__ int32_t lds_cnt[];
+  const int lane = threadIdx.x;
+  const int64_t ch = blockIdx.x;
+  int32_t* row = table + ch * (int64_t)C;
+  int32_t* cnt = USE_LDS ? lds_cnt : row;
+  if (USE_LDS) {
+    for (int c = lane; c < C; c += 64) cnt[c] = row[c];
+  }
+  __syncthreads();
+  const int64_t begin = ch * chunk;
+  const int64_t end = begin + chunk < A ? begin + chunk : A;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t seg = begin; seg < end; seg += 64) {
+    const int64_t a = seg + lane;
+    const bool valid = a < end;
+    const int32_t v = valid ? phys[a] : 0;
+    uint64_t mask = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (v >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      mask &= bit ? m : ~m;
+    }
+    int32_t base = 0;
+    if (valid) {
+      // The global-table counters are read and written by this wave only;
+      // device-scope atomics keep every access at L2, in program order.
+      base = USE_LDS ? cnt[v] : __hip_atomic_load(&cnt[v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (valid) {
+      pos[a] = base + __popcll(mask & lt_mask);
+      const int leader = 63 - __clzll(mask);
+      if (lane == leader) {
+        if (USE_LDS) cnt[v] = base + __popcll(mask);
+        else __hip_atomic_store(&cnt[v], base + __popcll(mask), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+int launch_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t src_const,
+                 int32_t S, int32_t E, int64_t A, int32_t K, int32_t C, int32_t* phys,
+                 int32_t* counts, int32_t* offsets, int32_t* pos, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream) {
+  if (C <= 0 || C > kRouteMaxSlots || A < 0 || K <= 0) return PMX_ERR_ARG;
+  if (!counts || !offsets || !workspace) return PMX_ERR_ARG;
+  if (A > 0 && (!sel || !phys || !pos)) return PMX_ERR_ARG;
+  if (M != nullptr && (S <= 0 || E <= 0)) return PMX_ERR_ARG;
+  if (workspace_bytes < route_ws_bytes(A, C)) return PMX_ERR_ARG;
+  int32_t* status = reinterpret_cast<int32_t*>(workspace);
+  int32_t* table = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kStatusBytes);
+  RouteGeom g = route_geom(A);
+  route_status_clear_kernel<<<1, 64, 0, stream>>>(status);
+  PMX_LAUNCH_CHECK();
+  const bool lds = C <= kRouteLdsMaxSlots;
+  const size_t lds_bytes = lds ? (size_t)C * sizeof(int32_t) : 0;
+  if (A == 0) {
+    // No assignments: the table is one zero row; the scan still writes
+    // counts and offsets.
+    fill_i32_kernel<<<(unsigned)((C + 255) / 256), 256, 0, stream>>>(table, C, 0);
+  } else if (lds) {
+    route_hist_kernel<true><<<(unsigned)g.nchunks, 64, lds_bytes, stream>>>(
+        sel, M, src, src_const, S, E, K, C, A, g.chunk, phys, table, status);
+  } else {
+    route_hist_kernel<false><<<(unsigned)g.nchunks, 64, 0, stream>>>(
+        sel, M, src, src_const, S, E, K, C, A, g.chunk, phys, table, status);
+  }
+  PMX_LAUNCH_CHECK();
+  route_scan_kernel<<<1, 1024, 0, stream>>>(table, g.nchunks, C, counts, offsets);
+  PMX_LAUNCH_CHECK();
+  if (A > 0) {
+    int nbits = 1;
+    while ((1 << nbits) < C) ++nbits;
+    if (lds) {
+      route_rank_kernel<true><<<(unsigned)g.nchunks, 64, lds_bytes, stream>>>(phys, table, C, A, g.chunk,
+                                                                             nbits, pos);
+    } else {
+      route_rank_kernel<false><<<(unsigned)g.nchunks, 64, 0, stream>>>(phys, table, C, A, g.chunk, nbits,
+                                                                      pos);
+    }
+    PMX_LAUNCH_CHECK();
+  }
+  return PMX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Row movement.  One block per token row; 16-byte accesses when H % 8 == 0.
+// ---------------------------------------------------------------------------
+
+inline unsigned row_threads(int64_t H) {
+  int64_t v = (H + 7) / 8;
+  v = (v + 63) / 64 * 64;
+  if (v < 64) v = 64;
+  if (v > 256) v = 256;
+  return (unsigned)v;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void scatter_rows_kernel(const bf16_t* __restrict__ X,
+                                                           const int32_t* __restrict__ pos, int32_t K,
+                                                           int64_t H, bf16_t* __restrict__ Xp) {
+  const int64_t t = blockIdx.x;
+  const int32_t* p = pos + t * K;
+  if (VEC) {
+    const int64_t n8 = H / 8;
+    const uint4* src = reinterpret_cast<const uint4*>(X + t * H);
+    for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
+      const uint4 v = src[i];
+      for (int k = 0; k < K; ++k) reinterpret_cast<uint4*>(Xp + (int64_t)p[k] * H)[i] = v;
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
+      const bf16_t v = X[t * H + i];
+      for (int k = 0; k < K; ++k) Xp[(int64_t)p[k] * H + i] = v;
+    }
+  }
+}
+
+// out[t] = bf16( sum_k fp32(term_k) ), term_k = Y[pos] or bf16(Y[pos] * w).
+template <bool VEC, bool WEIGHTED>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const bf16_t* __restrict__ Y,
+                                                          const int32_t* __restrict__ pos,
+                                                          const bf16_t* __restrict__ w, int32_t K,
+                                                          int64_t H, bf16_t* __restrict__ out) {
+  const int64_t t = blockIdx.x;
+  const int32_t* p = pos + t * K;
+  if (VEC) {
+    const int64_t n8 = H / 8;
+    for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int k = 0; k < K; ++k) {
+        const uint4 v = reinterpret_cast<const uint4*>(Y + (int64_t)p[k] * H)[i];
+        float f[8];
+        unpack8(v, f);
+        if (WEIGHTED) {
+          const float wk = bf16_to_f32(w[t * K + k]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[j] += round_bf16(f[j] * wk);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[j] += f[j];
+        }
+      }
+      reinterpret_cast<uint4*>(out + t * H)[i] = pack8(acc);
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
+      float acc = 0.f;
+      for (int k = 0; k < K; ++k) {
+        const float f = bf16_to_f32(Y[(int64_t)p[k] * H + i]);
+        if (WEIGHTED) acc += round_bf16(f * bf16_to_f32(w[t * K + k]));
+        else acc += f;
+      }
+      out[t * H + i] = (bf16_t)f32_to_bf16(acc);
+    }
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void combine_bwd_kernel(const bf16_t* __restrict__ dout,
+                                                          const bf16_t* __restrict__ Y,
+                                                          const int32_t* __restrict__ pos,
+                                                          const bf16_t* __restrict__ w, int32_t K,
+                                                          int64_t H, bf16_t* __restrict__ dY,
+                                                          bf16_t* __restrict__ dw) {
+  __shared__ float red[4][kMaxTopK];
+  const int64_t t = blockIdx.x;
+  const int32_t* p = pos + t * K;
+  float part[kMaxTopK];
+#pragma unroll
+  for (int k = 0; k < kMaxTopK; ++k) part[k] = 0.f;
+  if (VEC) {
+    const int64_t n8 = H / 8;
+    for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
+      float d[8];
+      unpack8(reinterpret_cast<const uint4*>(dout + t * H)[i], d);
+#pragma unroll
+      for (int k = 0; k < kMaxTopK; ++k) {
+        if (k < K) {
+          const int64_t row = p[k];
+          const float wk = bf16_to_f32(w[t * K + k]);
+          float g[8], y[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) g[j] = d[j] * wk;
+          reinterpret_cast<uint4*>(dY + row * H)[i] = pack8(g);
+          unpack8(reinterpret_cast<const uint4*>(Y + row * H)[i], y);
+          float s = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) s += round_bf16(d[j] * y[j]);
+          part[k] += s;
+        }
+      }
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
+      const float d = bf16_to_f32(dout[t * H + i]);
+#pragma unroll
+      for (int k = 0; k < kMaxTopK; ++k) {
+        if (k < K) {
+          const int64_t row = p[k];
+          const float wk = bf16_to_f32(w[t * K + k]);
+          dY[row * H + i] = (bf16_t)f32_to_bf16(d * wk);
+          part[k] += round_bf16(d * bf16_to_f32(Y[row * H + i]));
+        }
+      }
+    }
+  }
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int nwaves = blockDim.x / 64;
+#pragma unroll
+  for (int k = 0; k < kMaxTopK; ++k) {
+    if (k < K) {
+      const float s = wave_sum(part[k]);
+      if (lane == 0) red[wave][k] = s;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < (unsigned)K) {
+    float s = 0.f;
+    for (int wv = 0; wv < nwaves; ++wv) s += red[wv][threadIdx.x];
+    dw[t * K + threadIdx.x] = (bf16_t)f32_to_bf16(s);
+  }
+}
+
+// order[pos[i]] = i : the inverse of the stable scatter index.
+__global__ void invert_kernel(const int32_t* __restrict__ pos, int64_t N, int32_t* __restrict__ order) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < N) order[pos[i]] = (int32_t)i;
+}
+
+// out[r] = sum_{j in [off[r], off[r+1])} src[order[j]]  (fp32, bf16 store).
+template <bool VEC>
+__global__ __launch_bounds__(256) void segment_rows_kernel(const bf16_t* __restrict__ src,
+                                                           const int32_t* __restrict__ order,
+                                                           const int32_t* __restrict__ off, int64_t H,
+                                                           bf16_t* __restrict__ out) {
+  const int64_t r = blockIdx.x;
+  const int32_t b = off[r], e = off[r + 1];
+  if (VEC) {
+    const int64_t n8 = H / 8;
+    for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int32_t j = b; j < e; ++j) {
+        float f[8];
+        unpack8(reinterpret_cast<const uint4*>(src + (int64_t)order[j] * H)[i], f);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] += f[q];
+      }
+      reinterpret_cast<uint4*>(out + r * H)[i] = pack8(acc);
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
+      float acc = 0.f;
+      for (int32_t j = b; j < e; ++j) acc += bf16_to_f32(src[(int64_t)order[j] * H + i]);
+      out[r * H + i] = (bf16_t)f32_to_bf16(acc);
+    }
+  }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* pmx_version(void) { return "placemoe_amd 0.1.0 gfx950"; }
+
+const char* pmx_error_string(int code) {
+  switch (code) {
+    case PMX_OK: return "ok";
+    case PMX_ERR_HIP: return "HIP runtime error";
+    case PMX_ERR_ARG: return "invalid argument";
+    case PMX_ERR_SHAPE: return "unsupported shape";
+    case PMX_ERR_RANGE: return "index out of range";
+    default: return "unknown error";
+  }
+}
+
+size_t pmx_route_workspace_bytes(int64_t num_assign, int32_t num_slots) {
+  if (num_assign < 0 || num_slots <= 0) return 0;
+  return route_ws_bytes(num_assign, num_slots);
+}
+
+int pmx_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t src_const, int32_t S,
+              int32_t E, int64_t T, int32_t K, int32_t C, int32_t* phys, int32_t* counts,
+              int32_t* offsets, int32_t* pos, void* workspace, size_t workspace_bytes,
+              pmx_stream_t stream) {
+  if (T < 0 || K <= 0) return PMX_ERR_ARG;
+  if (M == nullptr && src != nullptr) return PMX_ERR_ARG;
+  return launch_route(sel, M, src, src_const, S, E, T * K, K, C, phys, counts, offsets, pos, workspace,
+                      workspace_bytes, stream);
+}
+
+int pmx_route_status(const void* workspace, int32_t* status_host, pmx_stream_t stream) {
+  if (!workspace || !status_host) return PMX_ERR_ARG;
+  hipError_t e = hipMemcpyAsync(status_host, workspace, sizeof(int32_t), hipMemcpyDeviceToHost, stream);
+  if (e != hipSuccess) return PMX_ERR_HIP;
+  return pmx_status(hipStreamSynchronize(stream));
+}
+
+int pmx_moe_scatter(const void* X, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* Xp,
+                    pmx_stream_t stream) {
+  if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
+  if (T == 0 || H == 0) return PMX_OK;
+  if (!X || !pos || !Xp) return PMX_ERR_ARG;
+  const unsigned th = row_threads(H);
+  if (H % 8 == 0 && aligned16(X) && aligned16(Xp)) {
+    scatter_rows_kernel<true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp);
+  } else {
+    scatter_rows_kernel<false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp);
+  }
+  PMX_LAUNCH_CHECK();
+  return PMX_OK;
+}
+
+int pmx_moe_gather(const void* Y, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* out,
+                   pmx_stream_t stream) {
+  if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
+  if (T == 0 || H == 0) return PMX_OK;
+  if (!Y || !pos || !out) return PMX_ERR_ARG;
+  const unsigned th = row_threads(H);
+  if (H % 8 == 0 && aligned16(Y) && aligned16(out)) {
+    gather_rows_kernel<true, false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, nullptr, K, H,
+                                                                   (bf16_t*)out);
+  } else {
+    gather_rows_kernel<false, false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, nullptr, K, H,
+                                                                    (bf16_t*)out);
+  }
+  PMX_LAUNCH_CHECK();
+  return PMX_OK;
+}
+
+int pmx_combine_fwd(const void* Y, const int32_t* pos, const void* w, int64_t T, int32_t K, int64_t H,
+                    void* out, pmx_stream_t stream) {
+  if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
+  if (T == 0 || H == 0) return PMX_OK;
+  if (!Y || !pos || !w || !out) return PMX_ERR_ARG;
+  const unsigned th = row_threads(H);
+  if (H % 8 == 0 && aligned16(Y) && aligned16(out)) {
+    gather_rows_kernel<true, true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, (const bf16_t*)w,
+                                                                  K, H, (bf16_t*)out);
+  } else {
+    gather_rows_kernel<false, true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, (const bf16_t*)w,
+                                                                   K, H, (bf16_t*)out);
+  }
+  PMX_LAUNCH_CHECK();
+  return PMX_OK;
+}
+
+int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const void* w, int64_t T,
+                    int32_t K, int64_t H, void* dY, void* dw, pmx_stream_t stream) {
+  if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
+  if (K > kMaxTopK) return PMX_ERR_ARG;
+  if (T == 0) return PMX_OK;
+  if (!dout || !Y || !pos || !w || !dY || !dw) return PMX_ERR_ARG;
+  const unsigned th = row_threads(H);
+  if (H % 8 == 0 && aligned16(dout) && aligned16(Y) && aligned16(dY)) {
+    combine_bwd_kernel<true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos,
+                                                            (const bf16_t*)w, K, H, (bf16_t*)dY,
+                                                            (bf16_t*)dw);
+  } else {
+    combine_bwd_kernel<false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos,
+                                                             (const bf16_t*)w, K, H, (bf16_t*)dY,
+                                                             (bf16_t*)dw);
+  }
+  PMX_LAUNCH_CHECK();
+  return PMX_OK;
+}
+
+size_t pmx_segment_sum_workspace_bytes(int64_t num_src_rows, int64_t num_rows) {
+  if (num_src_rows < 0 || num_rows <= 0 || num_rows > kRouteMaxSlots) return 0;
+  const int64_t N = num_src_rows;
+  size_t b = route_ws_bytes(N, (int32_t)num_rows);
+  b = (b + 255) / 256 * 256;
+  // phys, pos, order: int32 [N] each; counts [R], offsets [R+1]
+  b += (size_t)(3 * N + 2 * num_rows + 1) * sizeof(int32_t) + 4 * 256;
+  return b;
+}
+
+int pmx_segment_sum(const void* source, const int64_t* index, int64_t N, int64_t H, int64_t num_rows,
+                    void* out, void* workspace, size_t workspace_bytes, pmx_stream_t stream) {
+  if (N < 0 || H < 0 || num_rows < 0) return PMX_ERR_ARG;
+  if (num_rows == 0) return N == 0 ? PMX_OK : PMX_ERR_ARG;
+  if (num_rows > kRouteMaxSlots) return PMX_ERR_SHAPE;
+  if (!out || !workspace) return PMX_ERR_ARG;
+  if (N > 0 && (!source || !index)) return PMX_ERR_ARG;
+  if (workspace_bytes < pmx_segment_sum_workspace_bytes(N, num_rows)) return PMX_ERR_ARG;
+  const int32_t R = (int32_t)num_rows;
+  char* ws = reinterpret_cast<char*>(workspace);
+  size_t route_b = (route_ws_bytes(N, R) + 255) / 256 * 256;
+  auto carve = [&](size_t n_int) {
+    int32_t* p = reinterpret_cast<int32_t*>(ws + route_b);
+    route_b += (n_int * sizeof(int32_t) + 255) / 256 * 256;
+    return p;
+  };
+  int32_t* phys = carve((size_t)N);
+  int32_t* pos = carve((size_t)N);
+  int32_t* order = carve((size_t)N);
+  int32_t* counts = carve((size_t)R);
+  int32_t* offsets = carve((size_t)R + 1);
+  int rc = launch_route(index, nullptr, nullptr, 0, 1, R, N, 1, R, phys, counts, offsets, pos, workspace,
+                        route_ws_bytes(N, R), stream);
+  if (rc != PMX_OK) return rc;
+  if (N > 0) {
+    invert_kernel<<<(unsigned)((N + 255) / 256), 256, 0, stream>>>(pos, N, order);
+    PMX_LAUNCH_CHECK();
+  }
+  if (H == 0) return PMX_OK;
+  const unsigned th = row_threads(H);
+  if (H % 8 == 0 && aligned16(source) && aligned16(out)) {
+    segment_rows_kernel<true><<<(unsigned)R, th, 0, stream>>>((const bf16_t*)source, order, offsets, H,
+                                                             (bf16_t*)out);
+  } else {
+    segment_rows_kernel<false><<<(unsigned)R, th, 0, stream>>>((const bf16_t*)source, order, offsets, H,
+                                                              (bf16_t*)out);
+  }
+  PMX_LAUNCH_CHECK();
+  return PMX_OK;
+}
+
+}  // extern "C"

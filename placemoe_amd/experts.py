@@ -1,0 +1,147 @@
+"""Autograd functions for one GPU's share of the PlaceMoE expert layer.
+
+Forward:  route (M table -> histogram -> scan -> stable scatter index) ->
+permute -> fc1 + SwiGLU -> fc2 -> router-weighted combine.
+Backward: combine gradient -> fc2 dgrad + SwiGLU backward -> fc2 wgrad ->
+fc1 dgrad -> fc1 wgrad -> unpermute gradient.
+
+Every step is a gfx950 kernel of ``libplacemoe_amd.so``; no step has a torch
+or CPU fallback.  The composition follows the reference's EP + PlaceMoE
+branch of ``group_gemm_fused_moe_forward``
+(veomni/ops/kernels/moe/group_gemm.py:669-857): ``M`` gather
+(``map_logical_to_physical``, veomni/distributed/moe/hiermoe/expert_swap.py:5831-5879),
+per-copy contiguous rows, ``EPMergedFc1GroupGemm`` / ``EPGroupGemm``
+(veomni/distributed/moe/moe_layer.py:147-547), router weights applied in the
+combine (``rank_dedup_combine``, veomni/distributed/moe/hiermoe/all_to_all.py:2539-2564).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import kernels
+
+
+class _ExpertLayerBase(torch.autograd.Function):
+    """Shared forward/backward; subclasses fix how fc1 weights are passed."""
+
+    @staticmethod
+    def _forward(ctx, hidden, routing_weights, selected, mapping, sources, source, w_gate, w_up, copy_stride,
+                 fc2_weight, split, recorder):
+        T, H = hidden.shape
+        C, H2, inter = fc2_weight.shape
+        assert H2 == H, f"down_proj hidden size {H2} != hidden size {H}"
+        r = kernels.route(selected, C, mapping=mapping, sources=sources, source=source)
+        if recorder is not None:
+            recorder(r.counts)
+        xp = kernels.moe_scatter(hidden, r.pos)
+        gu, act = kernels.gemm_fc1_swiglu(xp, w_gate, w_up, copy_stride, r.offsets, C, inter)
+        y = kernels.group_gemm_nt(act, fc2_weight, r.offsets)
+        out = kernels.combine_fwd(y, r.pos, routing_weights)
+        ctx.save_for_backward(xp, gu, act, y, r.pos, r.offsets, routing_weights, w_gate, w_up, fc2_weight)
+        ctx.split = split
+        ctx.inter = inter
+        ctx.routing = r
+        return out
+
+    @staticmethod
+    def _backward(ctx, grad_out):
+        xp, gu, act, y, pos, offsets, w, w_gate, w_up, fc2_weight = ctx.saved_tensors
+        grad_out = grad_out.contiguous()
+        need_w, need_x = ctx.needs_input_grad[1], ctx.needs_input_grad[0]
+        dy, dw = kernels.combine_bwd(grad_out, y, pos, w)
+        dg1 = kernels.gemm_fc2_dgrad_swiglu(dy, fc2_weight, gu, offsets)
+        d_fc2 = kernels.group_gemm_tn(dy, act, offsets) if ctx.fc2_needs_grad else None
+        d_fc1 = None
+        if ctx.fc1_needs_grad:
+            d_fc1 = kernels.group_gemm_tn(dg1, xp, offsets, split=ctx.inter if ctx.split else None)
+        dx = None
+        if need_x:
+            # Merged weights: w_gate is the whole [C, 2I, H] gate_up_proj.
+            dxp = kernels.group_gemm_nn(dg1, w_gate, offsets, b_second=w_up if ctx.split else None)
+            dx = kernels.moe_gather(dxp, pos)
+        return dx, (dw if need_w else None), d_fc1, d_fc2
+
+
+class HipMergedFc1ExpertLayer(_ExpertLayerBase):
+    """Merged ``gate_up_proj`` [C, 2I, H] (``EPMergedFc1GroupGemm`` layout)."""
+
+    @staticmethod
+    def forward(ctx, hidden, routing_weights, selected, mapping, sources, source, fc1_1_2_weight, fc2_weight,
+                recorder=None):
+        C, two_i, H = fc1_1_2_weight.shape
+        assert two_i % 2 == 0, f"Merged fc1_1_2_weight dim 1 must be even, got {two_i}"
+        inter = two_i // 2
+        assert fc1_1_2_weight.is_contiguous() and fc2_weight.is_contiguous(), "Noncontiguous weights"
+        w_up = fc1_1_2_weight.view(-1)[inter * H:]
+        ctx.fc1_needs_grad = ctx.needs_input_grad[6]
+        ctx.fc2_needs_grad = ctx.needs_input_grad[7]
+        return _ExpertLayerBase._forward(
+            ctx, hidden, routing_weights, selected, mapping, sources, source, fc1_1_2_weight, w_up,
+            2 * inter * H, fc2_weight, False, recorder,
+        )
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        dx, dw, d_fc1, d_fc2 = _ExpertLayerBase._backward(ctx, grad_out)
+        return dx, dw, None, None, None, None, d_fc1, d_fc2, None
+
+
+class HipSplitFc1ExpertLayer(_ExpertLayerBase):
+    """Split ``fc1_1`` (gate) and ``fc1_2`` (up) [C, I, H] (``EPGroupGemm`` layout)."""
+
+    @staticmethod
+    def forward(ctx, hidden, routing_weights, selected, mapping, sources, source, fc1_1_weight, fc1_2_weight,
+                fc2_weight, recorder=None):
+        C, inter, H = fc1_1_weight.shape
+        assert fc1_2_weight.shape == fc1_1_weight.shape, "fc1_1 and fc1_2 shapes differ"
+        assert fc1_1_weight.is_contiguous() and fc1_2_weight.is_contiguous() and fc2_weight.is_contiguous(), (
+            "Noncontiguous weights"
+        )
+        ctx.fc1_needs_grad = ctx.needs_input_grad[6] or ctx.needs_input_grad[7]
+        ctx.fc2_needs_grad = ctx.needs_input_grad[8]
+        return _ExpertLayerBase._forward(
+            ctx, hidden, routing_weights, selected, mapping, sources, source, fc1_1_weight, fc1_2_weight,
+            inter * H, fc2_weight, True, recorder,
+        )
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        dx, dw, d_fc1, d_fc2 = _ExpertLayerBase._backward(ctx, grad_out)
+        d_gate, d_up = d_fc1 if d_fc1 is not None else (None, None)
+        return dx, dw, None, None, None, None, d_gate, d_up, d_fc2, None
+
+
+def expert_layer(
+    hidden: torch.Tensor,
+    routing_weights: torch.Tensor,
+    selected_experts: torch.Tensor,
+    fc2_weight: torch.Tensor,
+    fc1_1_2_weight: torch.Tensor | None = None,
+    fc1_1_weight: torch.Tensor | None = None,
+    fc1_2_weight: torch.Tensor | None = None,
+    mapping: torch.Tensor | None = None,
+    sources: torch.Tensor | None = None,
+    source: int = 0,
+    recorder=None,
+) -> torch.Tensor:
+    """The full layer on one GPU: [T, H] -> [T, H], differentiable in hidden,
+    routing weights and the expert weights.
+
+    ``mapping`` [S, E] maps (source, logical expert) to a physical copy (slot)
+    of ``fc2_weight.shape[0]`` copies; None means slot == logical expert.
+    ``recorder(counts)`` receives the int32 per-copy token counts (on the device).
+    """
+    if fc1_1_2_weight is not None:
+        if fc1_1_weight is not None or fc1_2_weight is not None:
+            raise ValueError("Provide either split fc1 weights or merged fc1_1_2_weight, not both.")
+        return HipMergedFc1ExpertLayer.apply(
+            hidden, routing_weights, selected_experts, mapping, sources, source, fc1_1_2_weight, fc2_weight,
+            recorder,
+        )
+    if fc1_1_weight is None or fc1_2_weight is None:
+        raise ValueError("Split fc1 mode requires both fc1_1_weight and fc1_2_weight.")
+    return HipSplitFc1ExpertLayer.apply(
+        hidden, routing_weights, selected_experts, mapping, sources, source, fc1_1_weight, fc1_2_weight, fc2_weight,
+        recorder,
+    )

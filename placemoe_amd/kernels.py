@@ -1,0 +1,329 @@
+"""Torch-tensor wrappers around the gfx950 C ABI.
+
+Each wrapper checks device, dtype and contiguity (``AssertionError``, as the
+reference's Triton wrappers do), allocates outputs with ``torch.empty`` on the
+input's device, and enqueues the kernels on torch's current stream.  Nothing
+here synchronises the host except ``route_status``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _capi
+
+BF16 = torch.bfloat16
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_dev(*tensors: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        assert t.is_cuda, "placemoe_amd kernels need GPU tensors"
+        if dev is None:
+            dev = t.device
+        assert t.device == dev, f"tensors on different devices: {t.device} vs {dev}"
+    return dev
+
+
+def _bf16(name: str, t: torch.Tensor) -> None:
+    assert t.dtype == BF16, f"{name} must be bfloat16, got {t.dtype}"
+    assert t.is_contiguous(), f"{name} must be contiguous"
+
+
+# ---------------------------------------------------------------------------
+# Routing
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class Routing:
+    """Integer routing of one batch: every tensor is int32 on the device."""
+
+    phys: torch.Tensor  # [T, K] physical copy of each assignment
+    counts: torch.Tensor  # [C]
+    offsets: torch.Tensor  # [C+1] exclusive prefix; offsets[1:] is cumsum_M
+    pos: torch.Tensor  # [T, K] row of each assignment in the permuted buffer
+    workspace: torch.Tensor  # holds the routing status word
+
+    @property
+    def num_slots(self) -> int:
+        return int(self.counts.numel())
+
+
+def route(
+    selected: torch.Tensor,
+    num_slots: int,
+    mapping: torch.Tensor | None = None,
+    sources: torch.Tensor | None = None,
+    source: int = 0,
+) -> Routing:
+    """phys = mapping[source(t), selected]; counts; offsets; stable scatter index.
+
+    ``mapping`` is the source-aware ``M`` table [S, E] (int64 on the device),
+    or None for the identity map.  ``sources`` is an int64 [T] per-token source
+    id; without it every token uses ``source`` (the reference's ``ep_rank``).
+    """
+    dev = _check_dev(selected, mapping, sources)
+    sel = selected if selected.dim() == 2 else selected.reshape(-1, 1)
+    sel = sel.to(torch.int64).contiguous()
+    T, K = sel.shape
+    C = int(num_slots)
+    if mapping is not None:
+        mapping = mapping.to(torch.int64).contiguous()
+        assert mapping.dim() == 2, "mapping must be [num_sources, num_experts]"
+        S, E = mapping.shape
+    else:
+        S, E = 1, C
+    if sources is not None:
+        assert mapping is not None, "per-token sources need a mapping table"
+        sources = sources.to(torch.int64).contiguous().reshape(-1)
+        assert sources.numel() == T, "sources must have one entry per token"
+    A = T * K
+    ws_bytes = _capi.load().pmx_route_workspace_bytes(A, C)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    phys = torch.empty((T, K), dtype=torch.int32, device=dev)
+    pos = torch.empty((T, K), dtype=torch.int32, device=dev)
+    counts = torch.empty(C, dtype=torch.int32, device=dev)
+    offsets = torch.empty(C + 1, dtype=torch.int32, device=dev)
+    _capi.call(
+        "pmx_route", _ptr(sel), _ptr(mapping), _ptr(sources), int(source), S, E, T, K, C,
+        _ptr(phys), _ptr(counts), _ptr(offsets), _ptr(pos), _ptr(ws), ws_bytes, _stream(dev),
+    )
+    return Routing(phys=phys, counts=counts, offsets=offsets, pos=pos, workspace=ws)
+
+
+def route_status(r: Routing) -> int:
+    """0 if every id was inside its table (synchronises the stream)."""
+    out = ctypes.c_int32(-1)
+    _capi.call("pmx_route_status", _ptr(r.workspace), ctypes.byref(out), _stream(r.workspace.device))
+    return int(out.value)
+
+
+# ---------------------------------------------------------------------------
+# Row movement
+# ---------------------------------------------------------------------------
+
+
+def moe_scatter(x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+    """Xp[pos[t,k]] = x[t]  ->  [T*K, H]."""
+    dev = _check_dev(x, pos)
+    _bf16("x", x)
+    assert pos.dtype == torch.int32 and pos.is_contiguous()
+    T, H = x.shape
+    K = pos.shape[1]
+    out = torch.empty((T * K, H), dtype=x.dtype, device=dev)
+    _capi.call("pmx_moe_scatter", _ptr(x), _ptr(pos), T, K, H, _ptr(out), _stream(dev))
+    return out
+
+
+def moe_gather(y: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+    """out[t] = bf16(sum_k fp32(y[pos[t,k]]))  ->  [T, H]."""
+    dev = _check_dev(y, pos)
+    _bf16("y", y)
+    assert pos.dtype == torch.int32 and pos.is_contiguous()
+    T, K = pos.shape
+    H = y.shape[1]
+    out = torch.empty((T, H), dtype=y.dtype, device=dev)
+    _capi.call("pmx_moe_gather", _ptr(y), _ptr(pos), T, K, H, _ptr(out), _stream(dev))
+    return out
+
+
+def combine_fwd(y: torch.Tensor, pos: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """out[t] = bf16(sum_k fp32(bf16(y[pos[t,k]] * w[t,k])))."""
+    dev = _check_dev(y, pos, w)
+    _bf16("y", y)
+    _bf16("routing weights", w)
+    T, K = pos.shape
+    H = y.shape[1]
+    out = torch.empty((T, H), dtype=y.dtype, device=dev)
+    _capi.call("pmx_combine_fwd", _ptr(y), _ptr(pos), _ptr(w), T, K, H, _ptr(out), _stream(dev))
+    return out
+
+
+def combine_bwd(dout: torch.Tensor, y: torch.Tensor, pos: torch.Tensor, w: torch.Tensor):
+    """(dy [T*K,H], dw [T,K]) - the gradients of ``combine_fwd``."""
+    dev = _check_dev(dout, y, pos, w)
+    _bf16("grad_output", dout)
+    _bf16("y", y)
+    _bf16("routing weights", w)
+    T, K = pos.shape
+    H = y.shape[1]
+    dy = torch.empty_like(y)
+    dw = torch.empty((T, K), dtype=w.dtype, device=dev)
+    _capi.call(
+        "pmx_combine_bwd", _ptr(dout), _ptr(y), _ptr(pos), _ptr(w), T, K, H, _ptr(dy), _ptr(dw), _stream(dev)
+    )
+    return dy, dw
+
+
+def segment_sum(source: torch.Tensor, index: torch.Tensor, num_rows: int) -> torch.Tensor:
+    """out[r] = sum_{i: index[i]==r} source[i] in fp32, stored as bf16.
+
+    Mirrors ``segment_sum_dim0_fp32_to_source_dtype``: raises ``ValueError`` for
+    an index outside [0, num_rows) (this check synchronises the stream).
+    """
+    if source.ndim != 2 or index.ndim != 1:
+        raise ValueError("source must be 2D and index must be 1D.")
+    if int(source.shape[0]) != int(index.numel()):
+        raise ValueError("index length must match source rows.")
+    num_rows = int(num_rows)
+    if num_rows < 0:
+        raise ValueError(f"num_rows must be non-negative, got {num_rows}.")
+    dev = _check_dev(source)
+    _bf16("source", source)
+    N, H = source.shape
+    out = torch.empty((num_rows, H), dtype=source.dtype, device=dev)
+    if num_rows == 0:
+        if N != 0:
+            raise ValueError("non-empty source cannot be reduced into zero rows.")
+        return out
+    idx = index.to(device=dev, dtype=torch.int64).contiguous()
+    ws_bytes = _capi.load().pmx_segment_sum_workspace_bytes(N, num_rows)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _capi.call(
+        "pmx_segment_sum", _ptr(source), _ptr(idx), N, H, num_rows, _ptr(out), _ptr(ws), ws_bytes, _stream(dev)
+    )
+    status = ctypes.c_int32(-1)
+    _capi.call("pmx_route_status", _ptr(ws), ctypes.byref(status), _stream(dev))
+    if status.value != 0:
+        raise ValueError("index contains a row outside [0, num_rows).")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Grouped GEMM
+# ---------------------------------------------------------------------------
+
+
+def gemm_fc1_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, copy_stride: int,
+                    offsets: torch.Tensor, num_groups: int, inter: int):
+    """(gu [A,2I], act [A,I]) = SwiGLU fc1 over per-copy row groups."""
+    dev = _check_dev(x, w_gate, w_up, offsets)
+    _bf16("hidden", x)
+    A, H = x.shape
+    gu = torch.empty((A, 2 * inter), dtype=x.dtype, device=dev)
+    act = torch.empty((A, inter), dtype=x.dtype, device=dev)
+    _capi.call(
+        "pmx_gemm_fc1_swiglu_fwd", _ptr(x), _ptr(w_gate), _ptr(w_up), int(copy_stride), _ptr(offsets),
+        int(num_groups), A, H, int(inter), _ptr(gu), _ptr(act), _stream(dev),
+    )
+    return gu, act
+
+
+def group_gemm_nt(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
+    """C[rows of g] = a[rows of g] @ b[g]^T, b: [G, N, K]."""
+    dev = _check_dev(a, b, offsets)
+    _bf16("a", a)
+    _bf16("b", b)
+    G, N, K = b.shape
+    assert a.shape[1] == K, "a and b disagree on K"
+    assert offsets.numel() == G + 1
+    M = a.shape[0]
+    c = torch.empty((M, N), dtype=a.dtype, device=dev)
+    _capi.call("pmx_group_gemm_nt", _ptr(a), _ptr(b), _ptr(offsets), G, M, N, K, _ptr(c), _stream(dev))
+    return c
+
+
+def group_gemm_nn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor,
+                  b_second: torch.Tensor | None = None) -> torch.Tensor:
+    """C[rows of g] = a[rows of g] @ cat(b, b_second, dim=1)[g], b: [G, K(, +K2), N]."""
+    dev = _check_dev(a, b, offsets, b_second)
+    _bf16("a", a)
+    _bf16("b", b)
+    G, K0, N = b.shape
+    K = K0 + (b_second.shape[1] if b_second is not None else 0)
+    if b_second is not None:
+        _bf16("b_second", b_second)
+        assert b_second.shape[0] == G and b_second.shape[2] == N and b_second.shape[1] == K0
+    assert a.shape[1] == K, "a and b disagree on K"
+    assert offsets.numel() == G + 1
+    M = a.shape[0]
+    c = torch.empty((M, N), dtype=a.dtype, device=dev)
+    _capi.call(
+        "pmx_group_gemm_nn", _ptr(a), _ptr(b), _ptr(b_second), K0 * N, K0 if b_second is not None else 0,
+        _ptr(offsets), G, M, N, K, _ptr(c), _stream(dev),
+    )
+    return c
+
+
+def gemm_fc2_dgrad_swiglu(dy: torch.Tensor, w_down: torch.Tensor, gu: torch.Tensor,
+                          offsets: torch.Tensor) -> torch.Tensor:
+    """dG1 [A,2I] = SwiGLU backward of (dy @ w_down[g]) given the saved gate/up."""
+    dev = _check_dev(dy, w_down, gu, offsets)
+    _bf16("dy", dy)
+    _bf16("w_down", w_down)
+    _bf16("gu", gu)
+    G, H, I = w_down.shape
+    A = dy.shape[0]
+    assert dy.shape[1] == H and gu.shape == (A, 2 * I)
+    dg1 = torch.empty((A, 2 * I), dtype=dy.dtype, device=dev)
+    _capi.call(
+        "pmx_gemm_fc2_dgrad_swiglu_bwd", _ptr(dy), _ptr(w_down), _ptr(gu), _ptr(offsets), G, A, H, I,
+        _ptr(dg1), _stream(dev),
+    )
+    return dg1
+
+
+def group_gemm_tn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, split: int | None = None):
+    """C[g] = a[rows g]^T @ b[rows g] -> [G, M, N] (zeros for empty groups).
+
+    With ``split`` the result is returned as two tensors [G, split, N] and
+    [G, M - split, N] (split fc1 weight gradients).
+    """
+    dev = _check_dev(a, b, offsets)
+    _bf16("a", a)
+    _bf16("b", b)
+    M, N = a.shape[1], b.shape[1]
+    G = offsets.numel() - 1
+    if split is None:
+        c0 = torch.empty((G, M, N), dtype=a.dtype, device=dev)
+        _capi.call(
+            "pmx_group_gemm_tn", _ptr(a), _ptr(b), _ptr(offsets), G, M, N, _ptr(c0), None, M * N, 0, _stream(dev)
+        )
+        return c0
+    assert M - split == split, "split gradients must have equal halves"
+    c0 = torch.empty((G, split, N), dtype=a.dtype, device=dev)
+    c1 = torch.empty((G, split, N), dtype=a.dtype, device=dev)
+    _capi.call(
+        "pmx_group_gemm_tn", _ptr(a), _ptr(b), _ptr(offsets), G, M, N, _ptr(c0), _ptr(c1), split * N, split,
+        _stream(dev),
+    )
+    return c0, c1
+
+
+# ---------------------------------------------------------------------------
+# Replica fold
+# ---------------------------------------------------------------------------
+
+
+def replica_fold(grads: torch.Tensor, copy_offsets: torch.Tensor, copy_slots: torch.Tensor, num_experts: int,
+                 slot_tokens: torch.Tensor | None = None, writeback: bool = False) -> torch.Tensor:
+    """fp32 [E, ...] = sum over the active copies of each expert of ``grads`` [C, ...]."""
+    dev = _check_dev(grads, copy_offsets, copy_slots, slot_tokens)
+    _bf16("grads", grads)
+    assert copy_offsets.dtype == torch.int32 and copy_slots.dtype == torch.int32
+    C = grads.shape[0]
+    P = grads[0].numel() if C else 0
+    out = torch.empty((num_experts,) + tuple(grads.shape[1:]), dtype=torch.float32, device=dev)
+    if slot_tokens is not None:
+        slot_tokens = slot_tokens.to(torch.int64).contiguous()
+        assert slot_tokens.numel() == C
+    _capi.call(
+        "pmx_replica_fold", _ptr(grads), _ptr(copy_offsets), _ptr(copy_slots), _ptr(slot_tokens),
+        int(num_experts), C, P, ctypes.cast(out.data_ptr(), ctypes.POINTER(ctypes.c_float)),
+        1 if writeback else 0, _stream(dev),
+    )
+    return out

@@ -1,0 +1,56 @@
+"""The C-ABI library loads without a GPU and exports every entry point that
+include/placemoe_amd.h declares, with the binding table in sync."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from placemoe_amd import _capi, build
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "placemoe_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pmx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_path():
+    names = declared_functions()
+    for must in ("pmx_route", "pmx_moe_scatter", "pmx_gemm_fc1_swiglu_fwd", "pmx_group_gemm_tn",
+                 "pmx_combine_fwd", "pmx_combine_bwd", "pmx_replica_fold"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    if not _capi.LIB_PATH.exists():
+        build.build()
+    lib = ctypes.CDLL(str(_capi.LIB_PATH))
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"missing exports: {missing}"
+
+
+def test_binding_table_matches_header():
+    assert sorted(_capi.SIGNATURES) == declared_functions()
+
+
+def test_host_only_calls_without_gpu():
+    lib = _capi.load()
+    assert b"gfx950" in lib.pmx_version()
+    assert lib.pmx_error_string(_capi.PMX_ERR_SHAPE) == b"unsupported shape"
+    assert lib.pmx_route_workspace_bytes(131072, 160) >= 256 + 64 * 160 * 4
+    assert lib.pmx_route_workspace_bytes(-1, 4) == 0
+
+
+def test_argument_errors_are_codes_not_crashes():
+    lib = _capi.load()
+    # invalid sizes are rejected before any device work
+    assert lib.pmx_route(None, None, None, 0, 1, 1, 4, 2, 0, None, None, None, None, None, 0, None) == _capi.PMX_ERR_ARG
+    assert lib.pmx_group_gemm_nt(None, None, None, 0, 8, 8, 8, None, None) == _capi.PMX_ERR_ARG
+    assert lib.pmx_group_gemm_nt(None, None, None, 4, 8, 12, 8, None, None) == _capi.PMX_ERR_SHAPE
+    assert lib.pmx_combine_bwd(None, None, None, None, 4, 33, 8, None, None, None) == _capi.PMX_ERR_ARG
+    with pytest.raises(ValueError):
+        _capi.call("pmx_group_gemm_nt", None, None, None, 4, 8, 12, 8, None, None)
