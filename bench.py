@@ -88,6 +88,8 @@ def parse():
     p.add_argument("--cpu-sample-tokens", type=int, default=1024)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--profile-steps", type=int, default=5, help="extra steps timed per kernel with HIP events")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="first run a plain 1 GiB device copy (reference kernel for HBM-traffic counters)")
     return p.parse_args()
 
 
@@ -146,6 +148,14 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        # 2^29 bf16 = 1 GiB read + 1 GiB written by one elementwise copy kernel
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     wl = make_workload(args.config, device=dev)
     backward = not wl.meta.get("forward_only", False)
     T, K, H, I, C = wl.T, wl.K, wl.H, wl.I, wl.C
@@ -182,6 +192,10 @@ def main():
     _capi.set_timer(None)
     avg = timer.averages()
     kernels_ms = {label: avg.get((name, idx)) for name, idx, label in STAGES if (name, idx) in avg}
+    if not kernels_ms:
+        print(json.dumps({"metric": "MoE layer fwd+bwd ms", "value": round(ms_per_step, 4), "unit": "ms",
+                          "note": "no per-kernel timing (--profile-steps 0)"}), flush=True)
+        return 0
 
     flops = {"fc1_fwd": work["fc1_fwd_flops"], "fc2_fwd": work["fc2_fwd_flops"],
              "fc2_dgrad": work["fc2_dgrad_flops"], "fc2_wgrad": work["fc2_wgrad_flops"],
