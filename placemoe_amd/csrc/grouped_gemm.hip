@@ -6,29 +6,46 @@
 //   KIND_NN    A[a] @ B[g]                         (fc1 dgrad)
 //   KIND_DG2   dY[a] @ Wdown[g] with the SwiGLU backward epilogue (fc2 dgrad)
 //   KIND_TN    A[rows g]^T @ B[rows g]             (wgrad, ragged K)
-// Groups are the per-copy row ranges [offsets[g], offsets[g+1]).  A fixed
-// grid of blocks walks a tile list derived on the device from `offsets`, so
-// empty groups cost nothing and the host never reads the counts.
+// Groups are the per-copy row ranges [offsets[g], offsets[g+1]).  A grid of
+// one block per CU walks a tile list derived on the device from `offsets`,
+// so empty groups cost nothing and the host never reads the counts.
 //
-// Tiles are 128x128x64, 256 threads = 4 waves in a 2x2 arrangement, each wave
-// owning 64x64 of the output as 4x4 v_mfma_f32_16x16x32_bf16 tiles with fp32
-// accumulators.  Operands are staged through double-buffered LDS with K
-// contiguous per row (128-byte rows, 16-byte chunks XOR-swizzled by row so
-// that both the MFMA fragment reads and the transposing stores are free of
-// bank conflicts).  Operands that are N- or M-contiguous in HBM (dgrad
-// weights, wgrad activations) are loaded as 4x8 blocks with 16-byte reads and
-// transposed in registers on their way into LDS.
+// Block tile BM x 256 x 32 (BM = 128), 4 waves in a 2x2 arrangement, each
+// wave owning (BM/2) x 128 of the output as 32x32 tiles of
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulators.
+//
+// Operands stream HBM -> LDS with buffer_load ... lds (no VGPR staging)
+// through a 6-stage pipeline: five K-tiles are in flight while the sixth is
+// multiplied (about 2500 MFMA cycles of latency cover at one wave per SIMD).
+// The loads are issued as inline asm and waited for by hand (vmcnt), one
+// stage's worth of instructions per step.  Rows or columns
+// outside a group, outside N/M, or past the K tail are masked by buffer
+// range checks (an out-of-range offset loads zeros).
+//
+// LDS layouts, both XOR-swizzled in 16-byte chunks so that the fragment reads
+// are free of bank conflicts:
+//   K-contiguous operands (activation rows, fc1/fc2 weights): [row][32 k],
+//     64-byte rows, chunk c stored at c ^ ((row >> 2) & 3); fragments
+//     are ds_read_b128.
+//   M/N-contiguous operands (dgrad weights, both wgrad operands): [32 k][W],
+//     chunk c of k-row kk stored at c ^ 4*(kk & 3); fragments are pairs of
+//     ds_read_b64_tr_b16, which transpose 4x16 blocks on the way out of LDS.
 
 #include "common.h"
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BN = 256, BK = 32, NSTAGE = 6;
 constexpr int NTHREADS = 256;
-constexpr int kTileBytes = 128 * BK * 2;  // one operand tile in LDS
 constexpr int kMaxGroups = 2048;
+constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always fails the range check
+constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
 enum Kind { KIND_FC1 = 0, KIND_NT = 1, KIND_NN = 2, KIND_DG2 = 3, KIND_TN = 4 };
+
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+#define LDS_TR_PTR(p) ((__attribute__((address_space(3))) bf16x4_t*)(p))
 
 // Row-major bf16 operand whose rows may come from two tensors: rows below
 // `split` from p0, the rest from p1 (row - split); per-group strides gs0/gs1.
@@ -54,241 +71,576 @@ struct GemmParams {
   bf16_t* dg1;
 };
 
-__device__ __forceinline__ const bf16_t* row_ptr(const RowSrc& s, int64_t g, int64_t row) {
-  return row < s.split ? s.p0 + g * s.gs0 + row * s.ld : s.p1 + g * s.gs1 + (row - s.split) * s.ld;
-}
-
-__device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * 128 + ((chunk ^ ((row ^ (row >> 3)) & 7)) << 4);
-}
-
-__device__ __forceinline__ uint4 ld16(const bf16_t* p) { return *reinterpret_cast<const uint4*>(p); }
-
-// Store a K-contiguous staging register set: thread t owns chunk (t & 7) of
-// rows (t >> 3) + 32 i.
-__device__ __forceinline__ void store_kc(char* lds, const uint4 (&r)[4], int t) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(lds + lds_off((t >> 3) + 32 * i, t & 7)) = r[i];
-}
-
-// Store a transposed staging set: r[j] holds 8 consecutive columns
-// (c8 * 8 ..) of K-row k4 * 4 + j; LDS row = column, K contiguous.
-__device__ __forceinline__ void store_kn(char* lds, const uint4 (&r)[4], int c8, int k4) {
-  const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&r[0]);
-  const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&r[1]);
-  const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&r[2]);
-  const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&r[3]);
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const int q = c >> 1;
-    uint2 v;
-    if (c & 1) {
-      v.x = (w0[q] >> 16) | (w1[q] & 0xffff0000u);
-      v.y = (w2[q] >> 16) | (w3[q] & 0xffff0000u);
-    } else {
-      v.x = (w0[q] & 0xffffu) | (w1[q] << 16);
-      v.y = (w2[q] & 0xffffu) | (w3[q] << 16);
-    }
-    const int row = c8 * 8 + c;
-    *reinterpret_cast<uint2*>(lds + lds_off(row, k4 >> 1) + (k4 & 1) * 8) = v;
-  }
-}
-
 template <int KIND>
-struct TileCtx {
-  int64_t g;
-  int64_t row0, row_end;  // ragged-M: output rows.  KIND_TN: reduction rows.
-  int64_t mtile, ntile;
-  int64_t nk;
+constexpr bool a_is_mn() { return KIND == KIND_TN; }
+template <int KIND>
+constexpr bool b_is_mn() { return KIND == KIND_NN || KIND == KIND_DG2 || KIND == KIND_TN; }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+  const uint32_t n = bytes > 0x7fffffffull ? 0x7fffffffu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, (int)kRsrcWord3);
+}
+
+__device__ __forceinline__ int kc_swz(int row) { return (row >> 2) & 3; }
+
+// Per-tile operand description.  Each DMA instruction of this wave has a
+// tile-invariant per-lane byte offset `voff[q0]` (kOOB where the lane's chunk
+// lies outside the operand); the K-tile advance goes into the scalar offset.
+// K-contiguous operands whose K is not a multiple of 32 use `voff_tail` in
+// their last K-tile, which masks the chunks past K.
+//
+// Per K-tile a wave only adds to the scalar offset (and, for wgrad operands,
+// rebases one descriptor): every per-tile quantity is set up once per tile.
+struct Operand {
+  __amdgpu_buffer_rsrc_t r0, r1;  // K-contiguous: r1 holds fc1's up rows;
+                                  // MN weights: k-rows below / from `split`
+  const char* base;               // wgrad operands: the group's first row ...
+  uint32_t bytes;                 // ... and the bytes of its rows (descriptor rebased per K-tile)
+  uint32_t ldb;                   // bytes between consecutive (k-)rows
+  int32_t split;                  // MN weights: first k-row taken from r1
+  uint32_t split_bytes;           // split * ldb
+  int32_t ktail;                  // the partial last K-tile, -1 if none
+  uint32_t voff[4];
+  uint32_t voff_tail[4];          // voff with the lanes past K masked (K-tile ktail)
 };
 
-// Global -> registers for K-tile kt.
-template <int KIND>
-__device__ __forceinline__ void load_tile(const GemmParams& P, const TileCtx<KIND>& tc, int64_t kt, int t,
-                                          uint4 (&ra)[4], uint4 (&rb)[4]) {
-  const uint4 zero = make_uint4(0, 0, 0, 0);
-  const int64_t k0 = kt * BK;
-  if constexpr (KIND == KIND_TN) {
-    // Both operands are [row][m or n]; transposed staging.
-    const int c8 = (t & 7) | ((t >> 7) << 3);
-    const int k4 = (t >> 3) & 15;
-    const int64_t m = tc.mtile * BM + c8 * 8;
-    const int64_t n = tc.ntile * BN + c8 * 8;
+// Where one output tile lies: group, m/n tile, its rows (ragged kinds: the
+// tile's first row and the group's end), and its K-tile count.
+struct TileInfo {
+  int32_t g, mtile, ntile, row0, row_end, nk;
+};
+
+template <int KIND, int BM>
+struct Tile {
+  TileInfo i;
+  Operand A, B;
+};
+
+// Wave-uniform copies (SGPRs) of values every lane holds alike: tile
+// bookkeeping read from LDS or memory would otherwise stay in VGPRs, and
+// descriptor selections on it would become branches around each load.
+__device__ __forceinline__ int32_t uni(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uni64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// One buffer->LDS instruction: 64 lanes x 16 bytes land contiguously at `dst`
+// (M0 holds the wave's LDS address).  Written as inline asm so that the
+// compiler does not track it: its own LDS-DMA bookkeeping cannot tell the
+// pipeline stages apart and would wait for younger stages before every LDS
+// read.  Completion is tracked by hand (wait_loads) and published to the
+// other waves by block_barrier, both of which clobber memory; this asm does
+// not, so LDS reads of other stages may be scheduled across it.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)LDS_PTR(dst);
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(m0));
+}
+
+// An empty descriptor: every offset fails its range check and loads zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t empty_rsrc(const void* base) { return make_rsrc(base, 0); }
+
+// K-contiguous operand, R rows x 32 k: the wave issues R/64 instructions of
+// 16 rows x 64 bytes.  Lane i of instruction q fills row 16q + i/4, physical
+// chunk i%4, i.e. logical chunk (i%4) ^ swz(row).
+// FC1's virtual B rows alternate 64 gate rows (r0) and 64 up rows (r1), so
+// instruction q0 (rows 64*q0 .. 64*q0+63 over the four waves) reads up rows
+// exactly when q0 is odd.
+template <int R, bool SPLIT_ROWS>
+__device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
+  const uint32_t soff = live ? (uint32_t)kt * (BK * 2) : 0u;
+  const bool tail = kt == op.ktail;
+  const __amdgpu_buffer_rsrc_t none = empty_rsrc(op.base);
+  const __amdgpu_buffer_rsrc_t r0 = live ? op.r0 : none;
+  const __amdgpu_buffer_rsrc_t r1 = live ? op.r1 : none;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t kk = k0 + k4 * 4 + j;
-      const int64_t row = tc.row0 + kk;
-      const bool kv = row < tc.row_end;
-      ra[j] = (kv && m < P.M) ? ld16(P.a.p0 + row * P.a.ld + m) : zero;
-      rb[j] = (kv && n < P.N) ? ld16(P.b.p0 + row * P.b.ld + n) : zero;
+  for (int q0 = 0; q0 < R / 64; ++q0) {
+    const int q = q0 * 4 + wave;
+    dma16((SPLIT_ROWS && (q0 & 1)) ? r1 : r0, lds + q * 1024, tail ? op.voff_tail[q0] : op.voff[q0], soff);
+  }
+}
+
+// M/N-contiguous operand, 32 k-rows x W columns: the wave issues W/64
+// instructions of 512/W k-rows x 2W bytes.  Lane i of instruction q fills
+// k-row q*ROWS + i/CH, physical chunk i%CH = logical chunk ^ 4*(kk&3).
+// REBASE (wgrad): the descriptor starts at the K-tile's first row and ends
+// with the group, so rows past the group load zeros.  Otherwise (dgrad
+// weights) the K-tile advance is a scalar offset into r0 (k-rows below split)
+// or r1, and the lanes past K are masked in the last K-tile.
+template <int W, bool REBASE>
+__device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
+  constexpr int ROWS = 1024 / (2 * W);
+  if constexpr (REBASE) {
+    const uint32_t skip = (uint32_t)kt * BK * op.ldb;
+    const uint64_t base = reinterpret_cast<uint64_t>(op.base) + (live ? skip : 0u);
+    const uint32_t bytes = (live && skip < op.bytes) ? op.bytes - skip : 0u;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const void*>(uni64((int64_t)base)), uni(bytes));
+#pragma unroll
+    for (int q0 = 0; q0 < W / 64; ++q0) {
+      const int q = q0 * 4 + wave;
+      dma16(rk, lds + q * 1024, op.voff[q0], 0u);
     }
   } else {
-    // A: activation rows, K contiguous.
-    const int kc = t & 7;
-    const int64_t kcol = k0 + kc * 8;
-    const bool kv = kcol < P.K;
+    const bool tail = kt == op.ktail;
+    const __amdgpu_buffer_rsrc_t none = empty_rsrc(op.base);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t row = tc.row0 + (t >> 3) + 32 * i;
-      ra[i] = (kv && row < tc.row_end) ? ld16(P.a.p0 + row * P.a.ld + kcol) : zero;
-    }
-    if constexpr (KIND == KIND_FC1) {
-      const int64_t j0 = tc.ntile * 64;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = (t >> 3) + 32 * i;
-        const int64_t j = j0 + (r >> 6) * 32 + (r & 31);
-        const int64_t prow = ((r >> 5) & 1) ? P.I + j : j;
-        rb[i] = (kv && j < P.I) ? ld16(row_ptr(P.b, tc.g, prow) + kcol) : zero;
-      }
-    } else if constexpr (KIND == KIND_NT) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t n = tc.ntile * BN + (t >> 3) + 32 * i;
-        rb[i] = (kv && n < P.N) ? ld16(row_ptr(P.b, tc.g, n) + kcol) : zero;
-      }
-    } else {  // KIND_NN, KIND_DG2: B is [k][n], N contiguous; transposed staging.
-      const int c8 = (t & 7) | ((t >> 7) << 3);
-      const int k4 = (t >> 3) & 15;
-      const int64_t n = tc.ntile * BN + c8 * 8;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t kk = k0 + k4 * 4 + j;
-        rb[j] = (kk < P.K && n < P.N) ? ld16(row_ptr(P.b, tc.g, kk) + n) : zero;
-      }
+    for (int q0 = 0; q0 < W / 64; ++q0) {
+      const int q = q0 * 4 + wave;
+      const int32_t k = kt * BK + q * ROWS;  // first k-row of the instruction
+      const bool second = k >= op.split;
+      const uint32_t soff = live ? (uint32_t)k * op.ldb - (second ? op.split_bytes : 0u) : 0u;
+      dma16(!live ? none : second ? op.r1 : op.r0, lds + q * 1024, tail ? op.voff_tail[q0] : op.voff[q0], soff);
     }
   }
 }
 
-template <int KIND>
-__device__ __forceinline__ void store_tile(char* As, char* Bs, int t, const uint4 (&ra)[4], const uint4 (&rb)[4]) {
-  const int c8 = (t & 7) | ((t >> 7) << 3);
-  const int k4 = (t >> 3) & 15;
-  if constexpr (KIND == KIND_TN) {
-    store_kn(As, ra, c8, k4);
-    store_kn(Bs, rb, c8, k4);
-  } else if constexpr (KIND == KIND_NN || KIND == KIND_DG2) {
-    store_kc(As, ra, t);
-    store_kn(Bs, rb, c8, k4);
-  } else {
-    store_kc(As, ra, t);
-    store_kc(Bs, rb, t);
+// Issue this wave's share of K-tile kt of a tile into `stage`.  `live` is
+// false for the pipeline slots past the block's last tile: they go through an
+// empty descriptor, so every step issues the same number of loads.
+template <int KIND, int BM>
+__device__ __forceinline__ void issue_stage(char* stage, const Tile<KIND, BM>& tc, int32_t kt, bool live, int wave) {
+  char* As = stage;
+  char* Bs = stage + BM * 64;
+  if constexpr (a_is_mn<KIND>()) dma_mn<BM, true>(As, tc.A, kt, live, wave);
+  else dma_kc<BM, false>(As, tc.A, kt, live, wave);
+  if constexpr (b_is_mn<KIND>()) dma_mn<BN, KIND == KIND_TN>(Bs, tc.B, kt, live, wave);
+  else dma_kc<BN, KIND == KIND_FC1>(Bs, tc.B, kt, live, wave);
+}
+
+// Fragment of a K-contiguous tile: lane l holds row (rb + l%32), k = ks*16 + (l/32)*8 + 0..7.
+__device__ __forceinline__ bf16x8_t frag_kc(const char* t, int rb, int ks, int lane) {
+  const int row = rb + (lane & 31);
+  const int chunk = ks * 2 + (lane >> 5);
+  return *reinterpret_cast<const bf16x8_t*>(t + row * 64 + ((chunk ^ kc_swz(row)) << 4));
+}
+
+// Fragment of an M/N-contiguous tile (W columns): lane l holds column
+// cb + l%32 at k = ks*16 + (l/32)*8 + 0..7, built from two transposing reads.
+// Within each 16-lane group, lane i addresses row i/4 and columns 4*(i%4)..+3
+// of a 4x16 block and receives column i of that block.
+template <int W>
+__device__ __forceinline__ bf16x8_t frag_mn(const char* t, int cb, int ks, int lane) {
+  const int gq = lane >> 4, i = lane & 15;
+  const int col = cb + 16 * (gq & 1) + (i & 3) * 4;
+  const int c = col >> 3, half = (col >> 2) & 1;
+  bf16x4_t v[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int kk = ks * 16 + (gq >> 1) * 8 + h * 4 + (i >> 2);
+    const char* p = t + kk * (2 * W) + ((c ^ (4 * (kk & 3))) << 4) + half * 8;
+    v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_TR_PTR(p));
+  }
+  return bf16x8_t{v[0][0], v[0][1], v[0][2], v[0][3], v[1][0], v[1][1], v[1][2], v[1][3]};
+}
+
+// The wave's operand fragments of one 16-deep k-step of a stage.
+template <int BM>
+struct Frags {
+  bf16x8_t a[BM / 64], b[4];
+};
+
+template <int KIND, int BM>
+__device__ __forceinline__ void read_frags(const char* stage, int ks, int wm, int wn, int lane, Frags<BM>& f) {
+  const char* As = stage;
+  const char* Bs = stage + BM * 64;
+#pragma unroll
+  for (int mt = 0; mt < BM / 64; ++mt) {
+    const int rb = wm * (BM / 2) + mt * 32;
+    if constexpr (a_is_mn<KIND>()) f.a[mt] = frag_mn<BM>(As, rb, ks, lane);
+    else f.a[mt] = frag_kc(As, rb, ks, lane);
+  }
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int cb = wn * 128 + nt * 32;
+    if constexpr (b_is_mn<KIND>()) f.b[nt] = frag_mn<BN>(Bs, cb, ks, lane);
+    else f.b[nt] = frag_kc(Bs, cb, ks, lane);
   }
 }
 
-__device__ __forceinline__ void mma_tile(const char* As, const char* Bs, int wm, int wn, int lane,
-                                         f32x4_t (&acc)[4][4]) {
+template <int BM>
+__device__ __forceinline__ void mma_frags(const Frags<BM>& f, f32x16_t (&acc)[BM / 64][4]) {
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    bf16x8_t a[4], b[4];
-    const int chunk = ks * 4 + (lane >> 4);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-      a[mt] = *reinterpret_cast<const bf16x8_t*>(As + lds_off(wm * 64 + mt * 16 + (lane & 15), chunk));
+  for (int mt = 0; mt < BM / 64; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
-      b[nt] = *reinterpret_cast<const bf16x8_t*>(Bs + lds_off(wn * 64 + nt * 16 + (lane & 15), chunk));
+      acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mt], f.b[nt], acc[mt][nt], 0, 0, 0);
+}
+
+template <int BM>
+__device__ __forceinline__ void zero_acc(f32x16_t (&acc)[BM / 64][4]) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < BM / 64; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mt], b[nt], acc[mt][nt], 0, 0, 0);
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
+}
+
+// Output element i of acc[mt][nt] in lane l sits at row
+// (i/4)*8 + (l/32)*4 + i%4, column l%32 of the 32x32 tile.
+//
+// Epilogue: each wave stages its (BM/2) x 128 output tile in rounds of 16
+// rows as bf16 in its own 4 KB of LDS (row-major, 256-byte rows, 16-byte
+// chunks XOR-swizzled by bit 2 of the row so the two half-waves' 2-byte
+// stores use different banks), then reads each round back one 16-byte chunk
+// per lane and writes whole row segments.  A wave's LDS operations complete in
+// order, so a round may overwrite what the previous one read.
+constexpr int kStageRegion = 6144;  // bytes of a pipeline stage per wave (24 KB / 4)
+
+__device__ __forceinline__ int epi_off(int row, int col) {
+  return row * 256 + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + (col & 7) * 2;
+}
+
+// Round r: rows 16r .. 16r+15 of the wave's tile, i.e. acc[r/2][.][8*(r%2) .. +7].
+template <typename F>
+__device__ __forceinline__ void stage_round(char* region, int lane, int r, int ncols, F value) {
+  const int cl = lane & 31;
+  const int rq = (lane >> 5) * 4;
+  const int mt = r >> 1, i0 = (r & 1) * 8;
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii) {
+      if (nt * 32 < ncols) {
+        const int row = (ii >> 2) * 8 + rq + (ii & 3);
+        *reinterpret_cast<bf16_t*>(region + epi_off(row, nt * 32 + cl)) = (bf16_t)f32_to_bf16(value(mt, nt, i0 + ii));
+      }
+    }
+}
+
+__device__ __forceinline__ uint4 staged_chunk(const char* region, int row, int chunk) {
+  return *reinterpret_cast<const uint4*>(region + row * 256 + ((chunk ^ (((row >> 2) & 1) << 2)) << 4));
+}
+
+template <int KIND, int BM>
+__device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti, int wm, int wn, int lane,
+                                         const f32x16_t (&acc)[BM / 64][4], char* region) {
+  constexpr int WM = BM / 2;
+  // The lane index passes through an opaque move so that the epilogue's
+  // per-lane address arithmetic stays here instead of being hoisted out of
+  // the tile loop, where it would hold registers through every K step.
+  asm volatile("" : "+v"(lane));
+  const int cc = lane & 15;  // read-back chunk (8 columns) of the 128-column tile
+#pragma unroll
+  for (int r = 0; r < WM / 16; ++r) {
+    const int64_t rb = wm * WM + r * 16;  // first row of the round within the tile
+    if constexpr (KIND == KIND_FC1) {
+      // gate | up columns (bf16 GEMM outputs), then act = bf16(bf16(silu(gate)) * up)
+      const int64_t I = P.I;
+      const int64_t j0 = (int64_t)ti.ntile * 128 + wn * 64;
+      stage_round(region, lane, r, 128, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int rl = (lane >> 4) + 4 * q;
+        const int64_t row = ti.row0 + rb + rl;
+        const uint4 v = staged_chunk(region, rl, cc);
+        const int64_t j = j0 + (cc & 7) * 8;
+        if (row < ti.row_end && j < I) *reinterpret_cast<uint4*>(P.gu + row * 2 * I + (cc < 8 ? 0 : I) + j) = v;
+      }
+      stage_round(region, lane, r, 64, [&](int mt, int nt, int i) {
+        const float gb = round_bf16(acc[mt][nt][i]);
+        const float ub = round_bf16(acc[mt][nt + 2][i]);
+        return round_bf16(silu_f32(gb)) * ub;
+      });
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int rl = (lane >> 3) + 8 * q, c8 = lane & 7;
+        const int64_t row = ti.row0 + rb + rl;
+        const uint4 v = staged_chunk(region, rl, c8);
+        const int64_t j = j0 + c8 * 8;
+        if (row < ti.row_end && j < I) *reinterpret_cast<uint4*>(P.act + row * I + j) = v;
+      }
+    } else {
+      stage_round(region, lane, r, 128, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      const int64_t col = (int64_t)ti.ntile * BN + wn * 128 + cc * 8;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int rl = (lane >> 4) + 4 * q;
+        const uint4 v = staged_chunk(region, rl, cc);
+        if constexpr (KIND == KIND_TN) {
+          const int64_t m = (int64_t)ti.mtile * BM + rb + rl;
+          if (m < P.M && col < P.N) {
+            bf16_t* crow = m < P.csplit ? P.c0 + ti.g * P.cgs + m * P.ldc : P.c1 + ti.g * P.cgs + (m - P.csplit) * P.ldc;
+            *reinterpret_cast<uint4*>(crow + col) = v;
+          }
+        } else if constexpr (KIND == KIND_DG2) {
+          const int64_t row = ti.row0 + rb + rl;
+          const int64_t I = P.I;
+          if (row < ti.row_end && col < I) {
+            float dact[8], g[8], u[8], dgate[8], dup[8];
+            unpack8(v, dact);
+            unpack8(*reinterpret_cast<const uint4*>(P.gu + row * 2 * I + col), g);
+            unpack8(*reinterpret_cast<const uint4*>(P.gu + row * 2 * I + I + col), u);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float s = round_bf16(silu_f32(g[e]));
+              const float d_silu = round_bf16(dact[e] * u[e]);
+              const float sig = sigmoid_f32(g[e]);
+              dgate[e] = d_silu * (sig * (1.0f + g[e] * (1.0f - sig)));
+              dup[e] = s * dact[e];
+            }
+            *reinterpret_cast<uint4*>(P.dg1 + row * 2 * I + col) = pack8(dgate);
+            *reinterpret_cast<uint4*>(P.dg1 + row * 2 * I + I + col) = pack8(dup);
+          }
+        } else {
+          const int64_t row = ti.row0 + rb + rl;
+          if (row < ti.row_end && col < P.N) *reinterpret_cast<uint4*>(P.c0 + row * P.ldc + col) = v;
+        }
+      }
+    }
   }
 }
 
-template <int KIND>
-__device__ __forceinline__ void epilogue(const GemmParams& P, const TileCtx<KIND>& tc, int wm, int wn,
-                                         int lane, const f32x4_t (&acc)[4][4]) {
-  const int col_l = lane & 15;
-  const int row_q = (lane >> 4) * 4;
+// The partial last K-tile of a K of `K` (-1 if none) and its valid k.
+__device__ __forceinline__ void k_tail(int64_t K, int32_t& ktail, int32_t& krem) {
+  const int32_t kt_last = (int32_t)((K - 1) / BK);
+  krem = (int32_t)(K - (int64_t)kt_last * BK);  // a multiple of 8
+  ktail = krem < BK ? kt_last : -1;
+}
+
+// Per-lane offsets of a K-contiguous operand whose tile rows start at the
+// descriptor base (rows past the descriptor's end fail the range check).
+template <int R>
+__device__ __forceinline__ void kc_offsets(Operand& op, int wave, int lane, int64_t K) {
+  int32_t krem;
+  k_tail(K, op.ktail, krem);
+#pragma unroll
+  for (int q0 = 0; q0 < R / 64; ++q0) {
+    const int row = (q0 * 4 + wave) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ kc_swz(row);
+    op.voff[q0] = (uint32_t)row * op.ldb + (uint32_t)c * 16u;
+    op.voff_tail[q0] = c * 8 < krem ? op.voff[q0] : kOOB;
+  }
+}
+
+// Per-lane offsets of an M/N-contiguous operand, relative to the first k-row
+// of each instruction (REBASE: of the K-tile), columns col0.. of the tile.
+// Not REBASE: voff_tail also masks the k-rows past K of the last K-tile.
+template <int W, bool REBASE>
+__device__ __forceinline__ void mn_offsets(Operand& op, int wave, int lane, int64_t col0, int64_t ncols, int64_t K) {
+  constexpr int CH = W / 8, ROWS = 1024 / (2 * W);
+  int32_t krem = BK;
+  op.ktail = -1;
+  if constexpr (!REBASE) k_tail(K, op.ktail, krem);
+#pragma unroll
+  for (int q0 = 0; q0 < W / 64; ++q0) {
+    const int q = q0 * 4 + wave;
+    const int kk = lane / CH;  // k-row within the instruction
+    const int krow = q * ROWS + kk;
+    const int c = (lane % CH) ^ (4 * (krow & 3));
+    const int64_t col = col0 + c * 8;
+    const uint32_t r = REBASE ? krow : kk;
+    op.voff[q0] = col < ncols ? r * op.ldb + (uint32_t)col * 2u : kOOB;
+    op.voff_tail[q0] = krow < krem ? op.voff[q0] : kOOB;
+  }
+}
+
+// Describe the operands of one output tile.
+template <int KIND, int BM>
+__device__ __forceinline__ void setup_operands(const GemmParams& P, Tile<KIND, BM>& tc, int wave, int lane) {
+  // Opaque lane: keeps the per-lane offset arithmetic here (see epilogue).
+  asm volatile("" : "+v"(lane));
+  const TileInfo& ti = tc.i;
   if constexpr (KIND == KIND_TN) {
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t m = tc.mtile * BM + wm * 64 + mt * 16 + row_q + j;
-        if (m >= P.M) continue;
-        bf16_t* crow = m < P.csplit ? P.c0 + tc.g * P.cgs + m * P.ldc : P.c1 + tc.g * P.cgs + (m - P.csplit) * P.ldc;
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const int64_t n = tc.ntile * BN + wn * 64 + nt * 16 + col_l;
-          if (n < P.N) crow[n] = (bf16_t)f32_to_bf16(acc[mt][nt][j]);
-        }
-      }
-    }
-  } else if constexpr (KIND == KIND_FC1) {
-    const int64_t I = P.I;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t row = tc.row0 + wm * 64 + mt * 16 + row_q + j;
-        if (row >= tc.row_end) continue;
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          const int64_t col = tc.ntile * 64 + wn * 32 + nt * 16 + col_l;
-          if (col >= I) continue;
-          const float gb = round_bf16(acc[mt][nt][j]);
-          const float ub = round_bf16(acc[mt][nt + 2][j]);
-          const float s = round_bf16(silu_f32(gb));
-          P.act[row * I + col] = (bf16_t)f32_to_bf16(s * ub);
-          bf16_t* gurow = P.gu + row * 2 * I;
-          gurow[col] = (bf16_t)f32_to_bf16(gb);
-          gurow[I + col] = (bf16_t)f32_to_bf16(ub);
-        }
-      }
-    }
-  } else if constexpr (KIND == KIND_DG2) {
-    const int64_t I = P.I;
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t row = tc.row0 + wm * 64 + mt * 16 + row_q + j;
-        if (row >= tc.row_end) continue;
-        const bf16_t* gurow = P.gu + row * 2 * I;
-        bf16_t* drow = P.dg1 + row * 2 * I;
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const int64_t col = tc.ntile * BN + wn * 64 + nt * 16 + col_l;
-          if (col >= I) continue;
-          const float dact = round_bf16(acc[mt][nt][j]);
-          const float g = bf16_to_f32(gurow[col]);
-          const float u = bf16_to_f32(gurow[I + col]);
-          const float s = round_bf16(silu_f32(g));
-          const float d_silu = round_bf16(dact * u);
-          const float sig = sigmoid_f32(g);
-          drow[col] = (bf16_t)f32_to_bf16(d_silu * (sig * (1.0f + g * (1.0f - sig))));
-          drow[I + col] = (bf16_t)f32_to_bf16(s * dact);
-        }
-      }
-    }
+    // A: the group's rows, columns m of the tile; B: the group's rows, columns n.
+    const int64_t rows = ti.row_end - ti.row0;
+    tc.A.base = reinterpret_cast<const char*>(P.a.p0 + (int64_t)ti.row0 * P.a.ld);
+    tc.A.ldb = (uint32_t)(P.a.ld * 2);
+    tc.A.bytes = (uint32_t)(rows * P.a.ld * 2);
+    tc.B.base = reinterpret_cast<const char*>(P.b.p0 + (int64_t)ti.row0 * P.b.ld);
+    tc.B.ldb = (uint32_t)(P.b.ld * 2);
+    tc.B.bytes = (uint32_t)(rows * P.b.ld * 2);
+    mn_offsets<BM, true>(tc.A, wave, lane, (int64_t)ti.mtile * BM, P.M, 0);
+    mn_offsets<BN, true>(tc.B, wave, lane, (int64_t)ti.ntile * BN, P.N, 0);
   } else {
+    const int64_t rows = ti.row_end - ti.row0 < BM ? ti.row_end - ti.row0 : BM;
+    const bf16_t* a0 = P.a.p0 + (int64_t)ti.row0 * P.a.ld;
+    tc.A.base = reinterpret_cast<const char*>(a0);
+    tc.A.r0 = tc.A.r1 = make_rsrc(a0, (uint64_t)rows * P.a.ld * 2);
+    tc.A.ldb = (uint32_t)(P.a.ld * 2);
+    kc_offsets<BM>(tc.A, wave, lane, P.K);
+    const bf16_t* b0 = P.b.p0 + (int64_t)ti.g * P.b.gs0;
+    const bf16_t* b1 = P.b.p1 + (int64_t)ti.g * P.b.gs1;
+    tc.B.base = reinterpret_cast<const char*>(b0);
+    if constexpr (KIND == KIND_FC1) {
+      // virtual B rows: per 128 rows, 64 gate rows (r0) then 64 up rows (r1)
+      tc.B.r0 = make_rsrc(b0, (uint64_t)P.I * P.K * 2);
+      tc.B.r1 = make_rsrc(b1, (uint64_t)P.I * P.K * 2);
+      tc.B.ldb = (uint32_t)(P.K * 2);
+      int32_t krem;
+      k_tail(P.K, tc.B.ktail, krem);
+      const int64_t j0 = (int64_t)ti.ntile * 128;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t row = tc.row0 + wm * 64 + mt * 16 + row_q + j;
-        if (row >= tc.row_end) continue;
-        bf16_t* crow = P.c0 + row * P.ldc;
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const int64_t col = tc.ntile * BN + wn * 64 + nt * 16 + col_l;
-          if (col < P.N) crow[col] = (bf16_t)f32_to_bf16(acc[mt][nt][j]);
-        }
+      for (int q0 = 0; q0 < BN / 64; ++q0) {
+        const int row = (q0 * 4 + wave) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ kc_swz(row);
+        const int64_t j = j0 + (row >> 7) * 64 + (row & 63);
+        tc.B.voff[q0] = j < P.I ? (uint32_t)j * tc.B.ldb + (uint32_t)c * 16u : kOOB;
+        tc.B.voff_tail[q0] = c * 8 < krem ? tc.B.voff[q0] : kOOB;
       }
+    } else if constexpr (KIND == KIND_NT) {
+      // rows n of B[g] ([N][K]) from row ntile*BN on
+      const int64_t n0 = (int64_t)ti.ntile * BN;
+      tc.B.r0 = tc.B.r1 = make_rsrc(b0 + n0 * P.K, (uint64_t)(P.N - n0) * P.K * 2);
+      tc.B.ldb = (uint32_t)(P.K * 2);
+      kc_offsets<BN>(tc.B, wave, lane, P.K);
+    } else {
+      // B[g] is [K][N]; k-rows below split come from b0, the rest from b1
+      const int64_t split = P.b.split < P.K ? P.b.split : P.K;
+      tc.B.r0 = make_rsrc(b0, (uint64_t)split * P.N * 2);
+      tc.B.r1 = make_rsrc(b1, (uint64_t)(P.K - split) * P.N * 2);
+      tc.B.split = (int32_t)split;
+      tc.B.ldb = (uint32_t)(P.N * 2);
+      tc.B.split_bytes = (uint32_t)split * tc.B.ldb;
+      mn_offsets<BN, false>(tc.B, wave, lane, (int64_t)ti.ntile * BN, P.N, P.K);
     }
   }
 }
 
-template <int KIND>
-__global__ __launch_bounds__(NTHREADS, 2) void grouped_gemm_kernel(GemmParams P) {
-  __shared__ __attribute__((aligned(16))) char lds[4 * kTileBytes];
+// Zero gradient tile of an empty group (wgrad): 16-byte stores, no LDS.
+template <int BM>
+__device__ __forceinline__ void zero_tile(const GemmParams& P, const TileInfo& ti, int t) {
+  const uint4 z = make_uint4(0, 0, 0, 0);
+  for (int e = t; e < BM * (BN / 8); e += NTHREADS) {
+    const int64_t m = (int64_t)ti.mtile * BM + e / (BN / 8);
+    const int64_t n = (int64_t)ti.ntile * BN + (e % (BN / 8)) * 8;
+    if (m < P.M && n < P.N) {
+      bf16_t* crow = m < P.csplit ? P.c0 + ti.g * P.cgs + m * P.ldc : P.c1 + ti.g * P.cgs + (m - P.csplit) * P.ldc;
+      *reinterpret_cast<uint4*>(crow + n) = z;
+    }
+  }
+}
+
+// Scheduling pattern of one pipeline step (2 x 8 MFMAs, 2 x (BM/64 + 4)
+// fragment reads): alternate one MFMA and one LDS read, so that the reads of
+// the next k-step issue while the current one multiplies.
+template <int BM>
+__device__ __forceinline__ void interleave_reads_mfma() {
+  constexpr int NREAD = BM / 64 + 4, NMMA = (BM / 64) * 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int i = 0; i < NREAD; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NMMA - NREAD, 0);
+  }
+}
+
+// Tile order: bands of kBand consecutive m-tiles, walked n-tile by n-tile
+// (m fastest).  The 32 blocks of one XCD, which run consecutive tiles, then
+// cover 8 m-tiles x 4 n-tiles and share both operands through that XCD's L2:
+// 8 A + 4 B strips (128 KB per K-tile) instead of the 1-2 A + 16-28 B strips
+// of an n-fastest order over wide outputs.
+constexpr int64_t kBand = 8;
+
+__device__ __forceinline__ void band_order(int64_t t, int64_t mtiles, int64_t ntn, int64_t& m, int64_t& n) {
+  const int64_t band = t / (kBand * ntn);
+  const int64_t m0 = band * kBand;
+  const int64_t gm = mtiles - m0 < kBand ? mtiles - m0 : kBand;
+  const int64_t r = t - m0 * ntn;
+  n = r / gm;
+  m = m0 + (r - n * gm);
+}
+
+// The tile list: every kind but TN walks m-tiles of all groups (exclusive
+// prefix `tpre`, ntn n-tiles each); TN walks the tiles_per_group weight tiles
+// of each group, whose K is the group's row count.
+template <int KIND, int BM>
+__device__ __forceinline__ TileInfo decode_tile(const GemmParams& P, int64_t tile, const int32_t* tpre, int G,
+                                                int64_t ntn, int64_t tiles_per_group) {
+  TileInfo ti;
+  int64_t m, n;
+  if constexpr (KIND == KIND_TN) {
+    const int64_t g = tile / tiles_per_group;
+    band_order(tile - g * tiles_per_group, tiles_per_group / ntn, ntn, m, n);
+    ti.g = (int32_t)g;
+    ti.mtile = (int32_t)m;
+    ti.row0 = P.offsets[g];
+    ti.row_end = P.offsets[g + 1];
+    ti.nk = (ti.row_end - ti.row0 + BK - 1) / BK;
+  } else {
+    band_order(tile, tpre[G], ntn, m, n);
+    // Uniform binary search for the group holding m-tile m.
+    int lo = 0, hi = G;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (uni(tpre[mid]) <= m) lo = mid;
+      else hi = mid - 1;
+    }
+    ti.g = lo;
+    ti.mtile = (int32_t)m - uni(tpre[lo]);
+    ti.row0 = P.offsets[lo] + ti.mtile * BM;
+    ti.row_end = P.offsets[lo + 1];
+    ti.nk = (int32_t)((P.K + BK - 1) / BK);
+  }
+  ti.ntile = (int32_t)n;
+  ti.g = uni(ti.g);
+  ti.mtile = uni(ti.mtile);
+  ti.ntile = uni(ti.ntile);
+  ti.row0 = uni(ti.row0);
+  ti.row_end = uni(ti.row_end);
+  ti.nk = uni(ti.nk);
+  return ti;
+}
+
+// Wait until at most PENDING of this wave's vector memory operations (its
+// buffer->LDS loads, and any stores since) are in flight.
+template <int PENDING>
+__device__ __forceinline__ void wait_loads() {
+  static_assert(PENDING >= 0 && PENDING <= 63, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PENDING) : "memory");
+}
+
+// Same, and this wave's LDS reads and writes have completed.
+template <int PENDING>
+__device__ __forceinline__ void wait_loads_lds() {
+  static_assert(PENDING >= 0 && PENDING <= 63, "vmcnt is 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(PENDING) : "memory");
+}
+
+// Workgroup barrier that neither the compiler's memory model nor its
+// scheduler moves anything across: memory operations stay on their side (the
+// asm clobbers memory), and so do the MFMAs, so that every LDS read consumed
+// before the barrier has returned by the time the wave reaches it.
+__device__ __forceinline__ void block_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// One block per CU walks its tiles (slot, slot + grid, ...) as one stream of
+// K-tiles: the issue cursor runs AHEAD K-tiles in front of the multiply, into
+// the next tile, so a tile's first loads are in flight while the previous
+// tile is finished and written out.
+//
+// K-tile number p of the stream lives in stage p % NSTAGE.  Between barrier
+// p-1 (after which stream tile p is in LDS) and barrier p, a wave
+//   - refills the stage of stream tile p-2 with stream tile p+AHEAD: every
+//     wave consumed its reads of p-2 before reaching barrier p-1,
+//   - reads tile p's k-step 0 fragments while it multiplies k-step 1 of tile
+//     p-1, then tile p's k-step 1 fragments while it multiplies k-step 0 of
+//     tile p, so LDS latency hides behind MFMAs,
+//   - when tile p is the first K-tile of an output tile, first writes out the
+//     previous output tile through the stage of p-1, whose reads every wave
+//     completed before barrier p-1 (that barrier waits for LDS reads too),
+//   - waits for its loads of stream tile p+1 (p+2 .. p+AHEAD stay in flight).
+template <int KIND, int BM>
+__global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P) {
+  constexpr int STAGE_BYTES = (BM + BN) * 64;
+  constexpr int PER_STAGE = (BM + BN) / 64;  // DMA instructions per wave per stage
+  constexpr int AHEAD = NSTAGE - 2;
+  static_assert(4 * kStageRegion == STAGE_BYTES, "epilogue regions tile one stage");
+  __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE_BYTES];
   __shared__ int32_t tpre[kMaxGroups + 1];
   __shared__ int32_t scan_buf[NTHREADS];
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int wave = t >> 6;
+  const int wave = uni(t >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int G = P.G;
 
@@ -299,7 +651,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void grouped_gemm_kernel(GemmParams P)
     tiles_per_group = mtn * ntn;
     total = tiles_per_group * G;
   } else {
-    ntn = (KIND == KIND_FC1) ? (P.I + 63) / 64 : (P.N + BN - 1) / BN;
+    ntn = (KIND == KIND_FC1) ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
     // Exclusive prefix of m-tiles per group: 8 groups per thread, then a
     // block scan of the 256 partial sums.
     int32_t loc[8];
@@ -337,57 +689,94 @@ __global__ __launch_bounds__(NTHREADS, 2) void grouped_gemm_kernel(GemmParams P)
   int64_t slot = blockIdx.x;
   if ((grid & 7) == 0) slot = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
 
-  // Buffer b of the double buffer: A tile at lds + 2b*T, B tile right after.
+  // Consume cursor: the output tile being multiplied.  Tiles without K-tiles
+  // (wgrad of an empty group) are written as zeros on the way.
+  int64_t c_tile = slot;
+  TileInfo cur;
+  for (;; c_tile += grid) {
+    if (c_tile >= total) return;
+    cur = decode_tile<KIND, BM>(P, c_tile, tpre, G, ntn, tiles_per_group);
+    if (cur.nk > 0) break;
+    zero_tile<BM>(P, cur, t);
+  }
 
-  for (int64_t tile = slot; tile < total; tile += grid) {
-    TileCtx<KIND> tc;
-    if constexpr (KIND == KIND_TN) {
-      tc.g = tile / tiles_per_group;
-      const int64_t rem = tile - tc.g * tiles_per_group;
-      tc.mtile = rem / ntn;
-      tc.ntile = rem - tc.mtile * ntn;
-      tc.row0 = P.offsets[tc.g];
-      tc.row_end = P.offsets[tc.g + 1];
-      tc.nk = (tc.row_end - tc.row0 + BK - 1) / BK;
-    } else {
-      const int64_t mt_global = tile / ntn;
-      tc.ntile = tile - mt_global * ntn;
-      int lo = 0, hi = G;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (tpre[mid] <= mt_global) lo = mid;
-        else hi = mid - 1;
-      }
-      tc.g = lo;
-      tc.mtile = mt_global - tpre[lo];
-      tc.row0 = P.offsets[lo] + tc.mtile * BM;
-      tc.row_end = P.offsets[lo + 1];
-      tc.nk = (P.K + BK - 1) / BK;
-    }
-
-    f32x4_t acc[4][4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    if (tc.nk > 0) {
-      uint4 ra[4], rb[4];
-      load_tile<KIND>(P, tc, 0, t, ra, rb);
-      store_tile<KIND>(lds, lds + kTileBytes, t, ra, rb);
-      __syncthreads();
-      for (int64_t kt = 0; kt < tc.nk; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < tc.nk;
-        if (more) load_tile<KIND>(P, tc, kt + 1, t, ra, rb);
-        char* cbuf = lds + cur * 2 * kTileBytes;
-        char* nbuf = lds + (cur ^ 1) * 2 * kTileBytes;
-        mma_tile(cbuf, cbuf + kTileBytes, wm, wn, lane, acc);
-        if (more) store_tile<KIND>(nbuf, nbuf + kTileBytes, t, ra, rb);
-        __syncthreads();
+  // Issue cursor: AHEAD K-tiles in front, over the same tile sequence.
+  Tile<KIND, BM> it;
+  int64_t i_tile = c_tile;
+  int32_t i_kt = 0;
+  bool i_live = true;
+  it.i = cur;
+  setup_operands<KIND, BM>(P, it, wave, lane);
+  auto issue_next = [&](char* stage) {
+    issue_stage<KIND, BM>(stage, it, i_kt, i_live, wave);
+    if (!i_live || ++i_kt < it.i.nk) return;
+    i_kt = 0;
+    for (i_tile += grid; i_tile < total; i_tile += grid) {
+      it.i = decode_tile<KIND, BM>(P, i_tile, tpre, G, ntn, tiles_per_group);
+      if (it.i.nk > 0) {
+        setup_operands<KIND, BM>(P, it, wave, lane);
+        return;
       }
     }
-    epilogue<KIND>(P, tc, wm, wn, lane, acc);
+    i_live = false;
+  };
+
+#pragma unroll
+  for (int p = 0; p < AHEAD; ++p) issue_next(lds + p * STAGE_BYTES);
+  wait_loads<(AHEAD - 1) * PER_STAGE>();
+  block_barrier();
+
+  f32x16_t acc[BM / 64][4];
+  Frags<BM> f0, f1;
+  int cs = 0;  // stage of the stream K-tile being multiplied
+  auto next_stage = [](int c) { return c + 1 == NSTAGE ? 0 : c + 1; };
+  auto refill_stage = [](int c) { return c + AHEAD >= NSTAGE ? c + AHEAD - NSTAGE : c + AHEAD; };
+  for (;;) {
+    // Output tile `cur`; its first K-tile is in stage cs and in LDS.
+    zero_acc<BM>(acc);
+    issue_next(lds + refill_stage(cs) * STAGE_BYTES);
+    read_frags<KIND, BM>(lds + cs * STAGE_BYTES, 0, wm, wn, lane, f0);
+    read_frags<KIND, BM>(lds + cs * STAGE_BYTES, 1, wm, wn, lane, f1);
+    mma_frags<BM>(f0, acc);
+    for (int32_t kt = 1; kt < cur.nk; ++kt) {
+      wait_loads<(AHEAD - 1) * PER_STAGE>();
+      block_barrier();
+      cs = next_stage(cs);
+      char* stage = lds + cs * STAGE_BYTES;
+      issue_next(lds + refill_stage(cs) * STAGE_BYTES);
+      read_frags<KIND, BM>(stage, 0, wm, wn, lane, f0);
+      mma_frags<BM>(f1, acc);
+      read_frags<KIND, BM>(stage, 1, wm, wn, lane, f1);
+      mma_frags<BM>(f0, acc);
+      interleave_reads_mfma<BM>();
+    }
+    // Move the consume cursor on.
+    const TileInfo done = cur;
+    bool more = false;
+    for (c_tile += grid; c_tile < total; c_tile += grid) {
+      cur = decode_tile<KIND, BM>(P, c_tile, tpre, G, ntn, tiles_per_group);
+      if (cur.nk > 0) {
+        more = true;
+        break;
+      }
+      zero_tile<BM>(P, cur, t);
+    }
+    if (!more) {
+      // Drain the remaining (empty) loads; then every stage is free.
+      mma_frags<BM>(f1, acc);
+      wait_loads_lds<0>();
+      block_barrier();
+      epilogue<KIND, BM>(P, done, wm, wn, lane, acc, lds + wave * kStageRegion);
+      return;
+    }
+    // The next tile's first K-tile lands; every wave's reads of this tile's
+    // last stage have returned, so the epilogue may stage through it while
+    // the next AHEAD - 1 K-tiles are in flight.
+    wait_loads_lds<(AHEAD - 1) * PER_STAGE>();
+    block_barrier();
+    mma_frags<BM>(f1, acc);
+    epilogue<KIND, BM>(P, done, wm, wn, lane, acc, lds + cs * STAGE_BYTES + wave * kStageRegion);
+    cs = next_stage(cs);
   }
 }
 
@@ -401,14 +790,18 @@ int grid_size() {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
     g_num_cus = cus > 0 ? cus : 256;
   }
-  return g_num_cus * 2;
+  return g_num_cus;
 }
+
+// 128 x 256 block tiles: the 256-row variant's 256 accumulators per lane leave
+// the register allocator too little room and it spills.
+constexpr int kBM = 128;
 
 template <int KIND>
 int launch(const GemmParams& P, hipStream_t stream) {
   const int grid = grid_size();
   if (grid <= 0) return PMX_ERR_HIP;
-  grouped_gemm_kernel<KIND><<<grid, NTHREADS, 0, stream>>>(P);
+  grouped_gemm_kernel<KIND, kBM><<<grid, NTHREADS, 0, stream>>>(P);
   PMX_LAUNCH_CHECK();
   return PMX_OK;
 }
@@ -424,6 +817,9 @@ RowSrc one(const void* p, int64_t gs, int64_t ld) {
   return s;
 }
 
+// Buffer offsets are 32-bit: one descriptor covers at most 2 GiB.
+bool fits_rsrc(int64_t rows, int64_t ld) { return rows * ld * 2 < (int64_t)0x7fffffff; }
+
 }  // namespace
 
 extern "C" {
@@ -436,6 +832,7 @@ int pmx_gemm_fc1_swiglu_fwd(const void* X, const void* w_gate, const void* w_up,
   if (A == 0) return PMX_OK;
   if (!X || !w_gate || !w_up || !offsets || !gu || !act) return PMX_ERR_ARG;
   if (!a16(X) || !a16(w_gate) || !a16(w_up)) return PMX_ERR_SHAPE;
+  if (!fits_rsrc(I, H) || !fits_rsrc(kBM, H)) return PMX_ERR_SHAPE;
   GemmParams P = {};
   P.a = one(X, 0, H);
   P.b.p0 = static_cast<const bf16_t*>(w_gate);
@@ -460,6 +857,7 @@ int pmx_group_gemm_nt(const void* A, const void* B, const int32_t* offsets, int3
   if (M == 0) return PMX_OK;
   if (!A || !B || !offsets || !C) return PMX_ERR_ARG;
   if (!a16(A) || !a16(B)) return PMX_ERR_SHAPE;
+  if (!fits_rsrc(N, K) || !fits_rsrc(kBM, K)) return PMX_ERR_SHAPE;
   GemmParams P = {};
   P.a = one(A, 0, K);
   P.b = one(B, N * K, K);
@@ -480,11 +878,13 @@ int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_c
   if (M == 0) return PMX_OK;
   if (!A || !B0 || !offsets || !C) return PMX_ERR_ARG;
   if (!a16(A) || !a16(B0) || (B1 && !a16(B1))) return PMX_ERR_SHAPE;
+  if (!fits_rsrc(K, N) || !fits_rsrc(kBM, K)) return PMX_ERR_SHAPE;
   GemmParams P = {};
   P.a = one(A, 0, K);
   P.b = one(B0, b_copy_stride, N);
   if (B1 != nullptr) {
-    if (b_split <= 0 || b_split >= K) return PMX_ERR_ARG;
+    // one buffer->LDS instruction covers two k-rows of a 256-wide tile
+    if (b_split <= 0 || b_split >= K || (b_split & 1)) return PMX_ERR_ARG;
     P.b.p1 = static_cast<const bf16_t*>(B1);
     P.b.split = b_split;
   }
@@ -504,6 +904,7 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
   if (A == 0) return PMX_OK;
   if (!dY || !w_down || !gu || !offsets || !dG1) return PMX_ERR_ARG;
   if (!a16(dY) || !a16(w_down)) return PMX_ERR_SHAPE;
+  if (!fits_rsrc(H, I) || !fits_rsrc(kBM, H)) return PMX_ERR_SHAPE;
   GemmParams P = {};
   P.a = one(dY, 0, H);
   P.b = one(w_down, H * I, I);
