@@ -4,7 +4,6 @@
 //   KIND_FC1   X[a] @ [Wgate;Wup][g]^T with the SwiGLU forward epilogue
 //   KIND_NT    A[a] @ B[g]^T                       (fc2 forward)
 //   KIND_NN    A[a] @ B[g]                         (fc1 dgrad)
-//   KIND_DG2   dY[a] @ Wdown[g] with the SwiGLU backward epilogue (fc2 dgrad)
 //   KIND_TN    A[rows g]^T @ B[rows g]             (wgrad, ragged K)
 // Groups are the per-copy row ranges [offsets[g], offsets[g+1]).  A grid of
 // one block per CU walks a tile list derived on the device from `offsets`,
@@ -35,13 +34,17 @@
 
 namespace {
 
-constexpr int BN = 256, BK = 32, NSTAGE = 6;
+constexpr int BN = 256, BK = 32;
+// Pipeline stages of (BM + BN) x 32 bf16 that fit next to the group prefix
+// in 160 KB of LDS: 6 x 24 KB for 128-row tiles, 4 x 32 KB for 256-row tiles.
+template <int BM>
+constexpr int nstage() { return BM == 128 ? 6 : 4; }
 constexpr int NTHREADS = 256;
 constexpr int kMaxGroups = 2048;
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always fails the range check
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
-enum Kind { KIND_FC1 = 0, KIND_NT = 1, KIND_NN = 2, KIND_DG2 = 3, KIND_TN = 4 };
+enum Kind { KIND_FC1 = 0, KIND_NT = 1, KIND_NN = 2, KIND_TN = 4 };
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
@@ -62,19 +65,18 @@ struct GemmParams {
   const int32_t* offsets;
   int32_t G;
   int64_t M, N, K;  // ragged-M kinds: N, K used.  KIND_TN: M, N used.
-  int64_t I;        // SwiGLU width for KIND_FC1 / KIND_DG2
+  int64_t I;        // SwiGLU width for KIND_FC1
   bf16_t* c0;
   bf16_t* c1;
   int64_t ldc, cgs, csplit;
-  bf16_t* gu;  // written by KIND_FC1, read by KIND_DG2
+  bf16_t* gu;  // written by KIND_FC1
   bf16_t* act;
-  bf16_t* dg1;
 };
 
 template <int KIND>
 constexpr bool a_is_mn() { return KIND == KIND_TN; }
 template <int KIND>
-constexpr bool b_is_mn() { return KIND == KIND_NN || KIND == KIND_DG2 || KIND == KIND_TN; }
+constexpr bool b_is_mn() { return KIND == KIND_NN || KIND == KIND_TN; }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
   const uint32_t n = bytes > 0x7fffffffull ? 0x7fffffffu : (uint32_t)bytes;
@@ -267,6 +269,20 @@ __device__ __forceinline__ void mma_frags(const Frags<BM>& f, f32x16_t (&acc)[BM
       acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mt], f.b[nt], acc[mt][nt], 0, 0, 0);
 }
 
+// Compile-time loop: f(Int<I>{}) for I = B .. E-1, so that accumulator
+// indices stay constants however large the unrolled body grows.
+template <int V>
+struct Int {
+  static constexpr int value = V;
+};
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(Int<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 template <int BM>
 __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[BM / 64][4]) {
 #pragma unroll
@@ -286,7 +302,9 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[BM / 64][4]) {
 // stores use different banks), then reads each round back one 16-byte chunk
 // per lane and writes whole row segments.  A wave's LDS operations complete in
 // order, so a round may overwrite what the previous one read.
-constexpr int kStageRegion = 6144;  // bytes of a pipeline stage per wave (24 KB / 4)
+// Each wave stages its epilogue through a quarter of one pipeline stage.
+template <int BM>
+constexpr int stage_region() { return (BM + BN) * 64 / 4; }
 
 __device__ __forceinline__ int epi_off(int row, int col) {
   return row * 256 + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + (col & 7) * 2;
@@ -322,8 +340,8 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
   // the tile loop, where it would hold registers through every K step.
   asm volatile("" : "+v"(lane));
   const int cc = lane & 15;  // read-back chunk (8 columns) of the 128-column tile
-#pragma unroll
-  for (int r = 0; r < WM / 16; ++r) {
+  static_for<0, WM / 16>([&](auto round) {
+    constexpr int r = decltype(round)::value;
     const int64_t rb = wm * WM + r * 16;  // first row of the round within the tile
     if constexpr (KIND == KIND_FC1) {
       // gate | up columns (bf16 GEMM outputs), then act = bf16(bf16(silu(gate)) * up)
@@ -364,32 +382,15 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
             bf16_t* crow = m < P.csplit ? P.c0 + ti.g * P.cgs + m * P.ldc : P.c1 + ti.g * P.cgs + (m - P.csplit) * P.ldc;
             *reinterpret_cast<uint4*>(crow + col) = v;
           }
-        } else if constexpr (KIND == KIND_DG2) {
-          const int64_t row = ti.row0 + rb + rl;
-          const int64_t I = P.I;
-          if (row < ti.row_end && col < I) {
-            float dact[8], g[8], u[8], dgate[8], dup[8];
-            unpack8(v, dact);
-            unpack8(*reinterpret_cast<const uint4*>(P.gu + row * 2 * I + col), g);
-            unpack8(*reinterpret_cast<const uint4*>(P.gu + row * 2 * I + I + col), u);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float s = round_bf16(silu_f32(g[e]));
-              const float d_silu = round_bf16(dact[e] * u[e]);
-              const float sig = sigmoid_f32(g[e]);
-              dgate[e] = d_silu * (sig * (1.0f + g[e] * (1.0f - sig)));
-              dup[e] = s * dact[e];
-            }
-            *reinterpret_cast<uint4*>(P.dg1 + row * 2 * I + col) = pack8(dgate);
-            *reinterpret_cast<uint4*>(P.dg1 + row * 2 * I + I + col) = pack8(dup);
-          }
         } else {
           const int64_t row = ti.row0 + rb + rl;
           if (row < ti.row_end && col < P.N) *reinterpret_cast<uint4*>(P.c0 + row * P.ldc + col) = v;
         }
       }
     }
-  }
+    // Keep each round's loads and stores in their round (register pressure).
+    asm volatile("" ::: "memory");
+  });
 }
 
 // The partial last K-tile of a K of `K` (-1 if none) and its valid k.
@@ -614,27 +615,30 @@ __device__ __forceinline__ void block_barrier() {
 }
 
 // One block per CU walks its tiles (slot, slot + grid, ...) as one stream of
-// K-tiles: the issue cursor runs AHEAD K-tiles in front of the multiply, into
-// the next tile, so a tile's first loads are in flight while the previous
-// tile is finished and written out.
+// K-tiles: the issue cursor runs AHEAD = NSTAGE - 1 K-tiles in front of the
+// multiply, into the next tile, so a tile's first loads are in flight while
+// the previous tile is finished and written out.
 //
 // K-tile number p of the stream lives in stage p % NSTAGE.  Between barrier
 // p-1 (after which stream tile p is in LDS) and barrier p, a wave
-//   - refills the stage of stream tile p-2 with stream tile p+AHEAD: every
-//     wave consumed its reads of p-2 before reaching barrier p-1,
+//   - refills the stage of stream tile p-1 with tile p+AHEAD: every wave's
+//     reads of p-1 returned before barrier p-1 (each barrier waits for the
+//     wave's LDS reads too; they were issued under 16 MFMAs, so little waits),
 //   - reads tile p's k-step 0 fragments while it multiplies k-step 1 of tile
 //     p-1, then tile p's k-step 1 fragments while it multiplies k-step 0 of
 //     tile p, so LDS latency hides behind MFMAs,
-//   - when tile p is the first K-tile of an output tile, first writes out the
-//     previous output tile through the stage of p-1, whose reads every wave
-//     completed before barrier p-1 (that barrier waits for LDS reads too),
 //   - waits for its loads of stream tile p+1 (p+2 .. p+AHEAD stay in flight).
+// After an output tile's last K-tile the waves finish it and write it out
+// through that K-tile's stage (its reads are done), then pass one more
+// barrier before that stage is refilled.
 template <int KIND, int BM>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P) {
   constexpr int STAGE_BYTES = (BM + BN) * 64;
   constexpr int PER_STAGE = (BM + BN) / 64;  // DMA instructions per wave per stage
-  constexpr int AHEAD = NSTAGE - 2;
-  static_assert(4 * kStageRegion == STAGE_BYTES, "epilogue regions tile one stage");
+  constexpr int NSTAGE = nstage<BM>();
+  constexpr int AHEAD = NSTAGE - 1;
+  constexpr int REGION = stage_region<BM>();
+  static_assert(REGION >= 16 * 256, "an epilogue round stages 16 rows of 256 bytes");
   __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE_BYTES];
   __shared__ int32_t tpre[kMaxGroups + 1];
   __shared__ int32_t scan_buf[NTHREADS];
@@ -739,7 +743,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     read_frags<KIND, BM>(lds + cs * STAGE_BYTES, 1, wm, wn, lane, f1);
     mma_frags<BM>(f0, acc);
     for (int32_t kt = 1; kt < cur.nk; ++kt) {
-      wait_loads<(AHEAD - 1) * PER_STAGE>();
+      wait_loads_lds<(AHEAD - 1) * PER_STAGE>();
       block_barrier();
       cs = next_stage(cs);
       char* stage = lds + cs * STAGE_BYTES;
@@ -761,22 +765,48 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       }
       zero_tile<BM>(P, cur, t);
     }
-    if (!more) {
-      // Drain the remaining (empty) loads; then every stage is free.
-      mma_frags<BM>(f1, acc);
-      wait_loads_lds<0>();
-      block_barrier();
-      epilogue<KIND, BM>(P, done, wm, wn, lane, acc, lds + wave * kStageRegion);
-      return;
-    }
-    // The next tile's first K-tile lands; every wave's reads of this tile's
-    // last stage have returned, so the epilogue may stage through it while
-    // the next AHEAD - 1 K-tiles are in flight.
-    wait_loads_lds<(AHEAD - 1) * PER_STAGE>();
+    // More tiles: the next tile's first K-tile lands, and every wave's reads
+    // of this tile's last stage have returned, so the epilogue may stage
+    // through that stage while the next AHEAD - 1 K-tiles are in flight.
+    // Last tile: drain the remaining (empty) loads.
+    if (more) wait_loads_lds<(AHEAD - 1) * PER_STAGE>();
+    else wait_loads_lds<0>();
     block_barrier();
     mma_frags<BM>(f1, acc);
-    epilogue<KIND, BM>(P, done, wm, wn, lane, acc, lds + cs * STAGE_BYTES + wave * kStageRegion);
+    epilogue<KIND, BM>(P, done, wm, wn, lane, acc, lds + cs * STAGE_BYTES + wave * REGION);
+    if (!more) return;
+    // The next step refills this stage: every wave must be done with it.
+    block_barrier();
     cs = next_stage(cs);
+  }
+}
+
+// SwiGLU backward of fc2's dgrad, 8 columns per thread.  dG1 row r holds
+// dact in its up half on entry; gate/up are gu's halves.  Per element
+//   s = bf16(silu(g)), d_silu = bf16(dact * u), sig = sigmoid(g)
+//   dG1[gate] = d_silu * sig * (1 + g * (1 - sig)),  dG1[up] = s * dact
+// (swiglu_backward of the reference's group GEMM path; each thread reads the
+// dact chunk it then overwrites).
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const bf16_t* __restrict__ gu, bf16_t* dg1, uint32_t chunks,
+                                                         uint32_t total, int64_t ld) {
+  for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < total; e += gridDim.x * 256u) {
+    const uint32_t r = e / chunks;
+    const int64_t c = (int64_t)(e - r * chunks) * 8;
+    const int64_t row = (int64_t)r * ld, up = ld / 2;
+    float dact[8], g[8], u[8], dgate[8], dup[8];
+    unpack8(*reinterpret_cast<const uint4*>(dg1 + row + up + c), dact);
+    unpack8(*reinterpret_cast<const uint4*>(gu + row + c), g);
+    unpack8(*reinterpret_cast<const uint4*>(gu + row + up + c), u);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float s = round_bf16(silu_f32(g[q]));
+      const float d_silu = round_bf16(dact[q] * u[q]);
+      const float sig = sigmoid_f32(g[q]);
+      dgate[q] = d_silu * (sig * (1.0f + g[q] * (1.0f - sig)));
+      dup[q] = s * dact[q];
+    }
+    *reinterpret_cast<uint4*>(dg1 + row + c) = pack8(dgate);
+    *reinterpret_cast<uint4*>(dg1 + row + up + c) = pack8(dup);
   }
 }
 
@@ -793,9 +823,11 @@ int grid_size() {
   return g_num_cus;
 }
 
-// 128 x 256 block tiles: the 256-row variant's 256 accumulators per lane leave
-// the register allocator too little room and it spills.
-constexpr int kBM = 128;
+// 256 x 256 block tiles: a 32-deep K-tile (32 KB) feeds 2 MFLOP, half the
+// bytes per flop of 128 x 256 tiles; operand delivery from L2 is what bounds
+// this kernel, so that outweighs the coarser padding of ragged groups.  The
+// accumulators fill the 256 AGPRs.
+constexpr int kBM = 256;
 
 template <int KIND>
 int launch(const GemmParams& P, hipStream_t stream) {
@@ -903,8 +935,10 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
   if (H % 8 || I % 8) return PMX_ERR_SHAPE;
   if (A == 0) return PMX_OK;
   if (!dY || !w_down || !gu || !offsets || !dG1) return PMX_ERR_ARG;
-  if (!a16(dY) || !a16(w_down)) return PMX_ERR_SHAPE;
+  if (!a16(dY) || !a16(w_down) || !a16(gu) || !a16(dG1)) return PMX_ERR_SHAPE;
   if (!fits_rsrc(H, I) || !fits_rsrc(kBM, H)) return PMX_ERR_SHAPE;
+  if (A * (I / 8) > (int64_t)UINT32_MAX) return PMX_ERR_SHAPE;
+  // dact = dY @ Wdown[g] (bf16), written into the up half of dG1's rows ...
   GemmParams P = {};
   P.a = one(dY, 0, H);
   P.b = one(w_down, H * I, I);
@@ -912,10 +946,17 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
   P.G = G;
   P.N = I;
   P.K = H;
-  P.I = I;
-  P.gu = static_cast<bf16_t*>(const_cast<void*>(gu));
-  P.dg1 = static_cast<bf16_t*>(dG1);
-  return launch<KIND_DG2>(P, stream);
+  P.c0 = static_cast<bf16_t*>(dG1) + I;
+  P.ldc = 2 * I;
+  const int rc = launch<KIND_NN>(P, stream);
+  if (rc != PMX_OK) return rc;
+  // ... then the SwiGLU backward in place.
+  const uint32_t chunks = (uint32_t)(I / 8), total = (uint32_t)(A * (I / 8));
+  const uint32_t blocks = (total + 255) / 256 < 4096u ? (total + 255) / 256 : 4096u;
+  swiglu_bwd_kernel<<<blocks, 256, 0, stream>>>(static_cast<const bf16_t*>(gu), static_cast<bf16_t*>(dG1), chunks,
+                                                total, 2 * I);
+  PMX_LAUNCH_CHECK();
+  return PMX_OK;
 }
 
 int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
