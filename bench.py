@@ -32,6 +32,14 @@ import torch
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 
+# HBM bytes per launch of a workload's dominant kernel, measured in separate
+# rocprofv3 runs of this benchmark (FETCH_SIZE, then WRITE_SIZE, each scaled by
+# what the counter reads for a 1 GiB device copy: x2.00 and x1.00).  Counters
+# cannot be read from inside a timed run, so the figure is carried here.
+MEASURED_TRAFFIC_BYTES = {
+    ("qwen3", "fc1_fwd"): (2415 + 576) * 2**20,
+}
+
 # Entry-point call order inside one step; repeated names are told apart by
 # their occurrence index.
 STAGES = [
@@ -236,7 +244,7 @@ def main():
         "bandwidth_gbps": bandwidth,
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(dom_tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": MEASURED_TRAFFIC_BYTES.get((args.config, dominant))},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -122,7 +122,8 @@ int pmx_segment_sum(const void* source, const int64_t* index, int64_t N, int64_t
  * w_up + g*w_copy_stride, each [I, H] row-major.  A merged gate_up_proj
  * [G, 2I, H] is w_gate = W, w_up = W + I*H, w_copy_stride = 2*I*H; split
  * fc1_1/fc1_2 weights [G, I, H] use w_copy_stride = I*H.
- * G <= 4096; H and I must be multiples of 8. */
+ * 1 <= G <= 2048; H, I, N and K must be multiples of 8 and every tensor
+ * 16-byte aligned (PMX_ERR_SHAPE otherwise). */
 
 /* Forward fc1 with the SwiGLU epilogue:
  *   gu[a, 0:I] = bf16(X[a] @ Wgate[g]^T), gu[a, I:2I] = bf16(X[a] @ Wup[g]^T)
@@ -150,10 +151,12 @@ int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_c
                       int64_t b_split, const int32_t* offsets, int32_t G, int64_t M,
                       int64_t N, int64_t K, void* C, pmx_stream_t stream);
 
-/* dgrad fc2 with the SwiGLU backward epilogue:
+/* dgrad fc2 followed by the SwiGLU backward:
  *   dact = bf16(dY[a] @ down[g])                      ([A,I])
  *   dG1[a, 0:I] = d_gate, dG1[a, I:2I] = d_up         (silu_backward rounding)
- * dY [A,H], down [G,H,I], gu [A,2I] from the forward, dG1 [A,2I].
+ * dY [A,H], down [G,H,I], gu [A,2I] from the forward, dG1 [A,2I].  Two
+ * launches on `stream`: the GEMM leaves dact in dG1[a, I:2I], then an
+ * elementwise pass rewrites both halves in place (no workspace). */
  * Replaces the dgrad + silu_backward + cat of EPMergedFc1GroupGemm.backward
  * (veomni/distributed/moe/moe_layer.py:453-482). */
 int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void* gu,
