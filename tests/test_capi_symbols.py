@@ -18,6 +18,22 @@ def declared_functions():
     return sorted(set(re.findall(r"\b(pmx_[a-z0-9_]+)\s*\(", text)))
 
 
+@pytest.mark.parametrize("compiler,lang", [("gcc", "c"), ("g++", "c++")])
+def test_header_compiles_standalone(compiler, lang, tmp_path):
+    """A binding written against the header alone (cgo, ctypes generators, C
+    callers) must be able to include it: plain C and C++, no HIP headers."""
+    import shutil
+    import subprocess
+
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} not available")
+    src = tmp_path / ("t.c" if lang == "c" else "t.cpp")
+    src.write_text(f'#include "{HEADER}"\nint main(void) {{ return pmx_version() != 0 ? 0 : 1; }}\n')
+    proc = subprocess.run([compiler, "-fsyntax-only", "-Wall", "-Werror", "-x", lang, str(src)],
+                          capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr
+
+
 def test_header_declares_the_path():
     names = declared_functions()
     for must in ("pmx_route", "pmx_moe_scatter", "pmx_gemm_fc1_swiglu_fwd", "pmx_group_gemm_tn",
