@@ -3,23 +3,24 @@
 // One persistent kernel template serves every GEMM of the layer:
 //   KIND_FC1   X[a] @ [Wgate;Wup][g]^T with the SwiGLU forward epilogue
 //   KIND_NT    A[a] @ B[g]^T                       (fc2 forward)
-//   KIND_NN    A[a] @ B[g]                         (fc1 dgrad)
+//   KIND_NN    A[a] @ B[g]                         (fc1 and fc2 dgrad)
 //   KIND_TN    A[rows g]^T @ B[rows g]             (wgrad, ragged K)
 // Groups are the per-copy row ranges [offsets[g], offsets[g+1]).  A grid of
 // one block per CU walks a tile list derived on the device from `offsets`,
 // so empty groups cost nothing and the host never reads the counts.
 //
-// Block tile BM x 256 x 32 (BM = 128), 4 waves in a 2x2 arrangement, each
-// wave owning (BM/2) x 128 of the output as 32x32 tiles of
-// v_mfma_f32_32x32x16_bf16 with fp32 accumulators.
+// Block tile 256 x 256, K in steps of 32; 4 waves in a 2x2 arrangement, each
+// owning 128 x 128 of the output as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16
+// whose fp32 accumulators fill the 256 AGPRs.
 //
 // Operands stream HBM -> LDS with buffer_load ... lds (no VGPR staging)
-// through a 6-stage pipeline: five K-tiles are in flight while the sixth is
-// multiplied (about 2500 MFMA cycles of latency cover at one wave per SIMD).
-// The loads are issued as inline asm and waited for by hand (vmcnt), one
-// stage's worth of instructions per step.  Rows or columns
-// outside a group, outside N/M, or past the K tail are masked by buffer
-// range checks (an out-of-range offset loads zeros).
+// through four 32 KB stages, three K-tiles in flight while one is multiplied;
+// a block walks its tiles as one stream of K-tiles, so the next tile's first
+// loads overlap the current tile's end and epilogue.  The loads are issued as
+// inline asm, one per pinned group of two MFMAs and one fragment read, and
+// waited for by hand (vmcnt).  Rows or columns outside a group, outside N/M,
+// or past K are masked by buffer range checks (an out-of-range offset loads
+// zeros).
 //
 // LDS layouts, both XOR-swizzled in 16-byte chunks so that the fragment reads
 // are free of bank conflicts:
@@ -149,7 +150,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t empty_rsrc(const void* base) {
 // FC1's virtual B rows alternate 64 gate rows (r0) and 64 up rows (r1), so
 // instruction q0 (rows 64*q0 .. 64*q0+63 over the four waves) reads up rows
 // exactly when q0 is odd.
-template <int R, bool SPLIT_ROWS>
+template <int R, bool SPLIT_ROWS, int Q0B = 0, int Q0E = R / 64>
 __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
   const uint32_t soff = live ? (uint32_t)kt * (BK * 2) : 0u;
   const bool tail = kt == op.ktail;
@@ -157,7 +158,7 @@ __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt,
   const __amdgpu_buffer_rsrc_t r0 = live ? op.r0 : none;
   const __amdgpu_buffer_rsrc_t r1 = live ? op.r1 : none;
 #pragma unroll
-  for (int q0 = 0; q0 < R / 64; ++q0) {
+  for (int q0 = Q0B; q0 < Q0E; ++q0) {
     const int q = q0 * 4 + wave;
     dma16((SPLIT_ROWS && (q0 & 1)) ? r1 : r0, lds + q * 1024, tail ? op.voff_tail[q0] : op.voff[q0], soff);
   }
@@ -170,7 +171,7 @@ __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt,
 // with the group, so rows past the group load zeros.  Otherwise (dgrad
 // weights) the K-tile advance is a scalar offset into r0 (k-rows below split)
 // or r1, and the lanes past K are masked in the last K-tile.
-template <int W, bool REBASE>
+template <int W, bool REBASE, int Q0B = 0, int Q0E = W / 64>
 __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
   constexpr int ROWS = 1024 / (2 * W);
   if constexpr (REBASE) {
@@ -179,7 +180,7 @@ __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt,
     const uint32_t bytes = (live && skip < op.bytes) ? op.bytes - skip : 0u;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const void*>(uni64((int64_t)base)), uni(bytes));
 #pragma unroll
-    for (int q0 = 0; q0 < W / 64; ++q0) {
+    for (int q0 = Q0B; q0 < Q0E; ++q0) {
       const int q = q0 * 4 + wave;
       dma16(rk, lds + q * 1024, op.voff[q0], 0u);
     }
@@ -187,7 +188,7 @@ __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt,
     const bool tail = kt == op.ktail;
     const __amdgpu_buffer_rsrc_t none = empty_rsrc(op.base);
 #pragma unroll
-    for (int q0 = 0; q0 < W / 64; ++q0) {
+    for (int q0 = Q0B; q0 < Q0E; ++q0) {
       const int q = q0 * 4 + wave;
       const int32_t k = kt * BK + q * ROWS;  // first k-row of the instruction
       const bool second = k >= op.split;
@@ -200,14 +201,32 @@ __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt,
 // Issue this wave's share of K-tile kt of a tile into `stage`.  `live` is
 // false for the pipeline slots past the block's last tile: they go through an
 // empty descriptor, so every step issues the same number of loads.
-template <int KIND, int BM>
+// PART selects the operands: 0 = A, 1 = B, 2 = both.
+template <int KIND, int BM, int PART = 2>
 __device__ __forceinline__ void issue_stage(char* stage, const Tile<KIND, BM>& tc, int32_t kt, bool live, int wave) {
   char* As = stage;
   char* Bs = stage + BM * 64;
-  if constexpr (a_is_mn<KIND>()) dma_mn<BM, true>(As, tc.A, kt, live, wave);
-  else dma_kc<BM, false>(As, tc.A, kt, live, wave);
-  if constexpr (b_is_mn<KIND>()) dma_mn<BN, KIND == KIND_TN>(Bs, tc.B, kt, live, wave);
-  else dma_kc<BN, KIND == KIND_FC1>(Bs, tc.B, kt, live, wave);
+  if constexpr (PART != 1) {
+    if constexpr (a_is_mn<KIND>()) dma_mn<BM, true>(As, tc.A, kt, live, wave);
+    else dma_kc<BM, false>(As, tc.A, kt, live, wave);
+  }
+  if constexpr (PART != 0) {
+    if constexpr (b_is_mn<KIND>()) dma_mn<BN, KIND == KIND_TN>(Bs, tc.B, kt, live, wave);
+    else dma_kc<BN, KIND == KIND_FC1>(Bs, tc.B, kt, live, wave);
+  }
+}
+
+// Instruction Q0 of this wave's share of operand OPER (0 = A, 1 = B).
+template <int KIND, int BM, int OPER, int Q0>
+__device__ __forceinline__ void issue_one(char* stage, const Tile<KIND, BM>& tc, int32_t kt, bool live, int wave) {
+  if constexpr (OPER == 0) {
+    if constexpr (a_is_mn<KIND>()) dma_mn<BM, true, Q0, Q0 + 1>(stage, tc.A, kt, live, wave);
+    else dma_kc<BM, false, Q0, Q0 + 1>(stage, tc.A, kt, live, wave);
+  } else {
+    char* Bs = stage + BM * 64;
+    if constexpr (b_is_mn<KIND>()) dma_mn<BN, KIND == KIND_TN, Q0, Q0 + 1>(Bs, tc.B, kt, live, wave);
+    else dma_kc<BN, KIND == KIND_FC1, Q0, Q0 + 1>(Bs, tc.B, kt, live, wave);
+  }
 }
 
 // Fragment of a K-contiguous tile: lane l holds row (rb + l%32), k = ks*16 + (l/32)*8 + 0..7.
@@ -258,6 +277,30 @@ __device__ __forceinline__ void read_frags(const char* stage, int ks, int wm, in
     if constexpr (b_is_mn<KIND>()) f.b[nt] = frag_mn<BN>(Bs, cb, ks, lane);
     else f.b[nt] = frag_kc(Bs, cb, ks, lane);
   }
+}
+
+// Fragment J of a k-step: A fragments 0 .. BM/64-1, then B fragments 0..3.
+template <int KIND, int BM, int J>
+__device__ __forceinline__ void read_frag(const char* stage, int ks, int wm, int wn, int lane, Frags<BM>& f) {
+  constexpr int MT = BM / 64;
+  if constexpr (J < MT) {
+    const int rb = wm * (BM / 2) + J * 32;
+    if constexpr (a_is_mn<KIND>()) f.a[J] = frag_mn<BM>(stage, rb, ks, lane);
+    else f.a[J] = frag_kc(stage, rb, ks, lane);
+  } else {
+    const char* Bs = stage + BM * 64;
+    const int cb = wn * 128 + (J - MT) * 32;
+    if constexpr (b_is_mn<KIND>()) f.b[J - MT] = frag_mn<BN>(Bs, cb, ks, lane);
+    else f.b[J - MT] = frag_kc(Bs, cb, ks, lane);
+  }
+}
+
+// MFMAs I .. I+N-1 of a k-step (index mt * 4 + nt).
+template <int BM, int I, int N>
+__device__ __forceinline__ void mma_some(const Frags<BM>& f, f32x16_t (&acc)[BM / 64][4]) {
+#pragma unroll
+  for (int x = I; x < I + N; ++x)
+    acc[x / 4][x % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x / 4], f.b[x % 4], acc[x / 4][x % 4], 0, 0, 0);
 }
 
 template <int BM>
@@ -513,23 +556,6 @@ __device__ __forceinline__ void zero_tile(const GemmParams& P, const TileInfo& t
   }
 }
 
-// Scheduling pattern of one pipeline step (2 x 8 MFMAs, 2 x (BM/64 + 4)
-// fragment reads): alternate one MFMA and one LDS read, so that the reads of
-// the next k-step issue while the current one multiplies.
-template <int BM>
-__device__ __forceinline__ void interleave_reads_mfma() {
-  constexpr int NREAD = BM / 64 + 4, NMMA = (BM / 64) * 4;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-#pragma unroll
-    for (int i = 0; i < NREAD; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, NMMA - NREAD, 0);
-  }
-}
-
 // Tile order: bands of kBand consecutive m-tiles, walked n-tile by n-tile
 // (m fastest).  The 32 blocks of one XCD, which run consecutive tiles, then
 // cover 8 m-tiles x 4 n-tiles and share both operands through that XCD's L2:
@@ -711,8 +737,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   bool i_live = true;
   it.i = cur;
   setup_operands<KIND, BM>(P, it, wave, lane);
-  auto issue_next = [&](char* stage) {
-    issue_stage<KIND, BM>(stage, it, i_kt, i_live, wave);
+  auto advance_issue = [&]() {
     if (!i_live || ++i_kt < it.i.nk) return;
     i_kt = 0;
     for (i_tile += grid; i_tile < total; i_tile += grid) {
@@ -723,6 +748,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       }
     }
     i_live = false;
+  };
+  auto issue_next = [&](char* stage) {
+    issue_stage<KIND, BM>(stage, it, i_kt, i_live, wave);
+    advance_issue();
   };
 
 #pragma unroll
@@ -747,12 +776,28 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       block_barrier();
       cs = next_stage(cs);
       char* stage = lds + cs * STAGE_BYTES;
-      issue_next(lds + refill_stage(cs) * STAGE_BYTES);
-      read_frags<KIND, BM>(stage, 0, wm, wn, lane, f0);
-      mma_frags<BM>(f1, acc);
-      read_frags<KIND, BM>(stage, 1, wm, wn, lane, f1);
-      mma_frags<BM>(f0, acc);
-      interleave_reads_mfma<BM>();
+      char* refill = lds + refill_stage(cs) * STAGE_BYTES;
+      // One pinned group per A/B fragment: its load (every other group), the
+      // fragment read for the next k-step, and a slice of this k-step's
+      // MFMAs.  A load whose issue stalls in the texture unit then stalls
+      // while MFMAs run, instead of holding back a burst of them.
+      constexpr int NF = BM / 64 + 4, NM = (BM / 64) * 4, PER = NM / NF;
+      static_assert(NM % NF == 0 && NF % 2 == 0 && PER_STAGE == NF, "schedule shape");
+      static_for<0, NF>([&](auto jj) {
+        constexpr int j = decltype(jj)::value;
+        if constexpr (j % 2 == 0) issue_one<KIND, BM, 0, j / 2>(refill, it, i_kt, i_live, wave);
+        read_frag<KIND, BM, j>(stage, 0, wm, wn, lane, f0);
+        mma_some<BM, j * PER, PER>(f1, acc);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      static_for<0, NF>([&](auto jj) {
+        constexpr int j = decltype(jj)::value;
+        if constexpr (j % 2 == 0) issue_one<KIND, BM, 1, j / 2>(refill, it, i_kt, i_live, wave);
+        read_frag<KIND, BM, j>(stage, 1, wm, wn, lane, f1);
+        mma_some<BM, j * PER, PER>(f0, acc);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      advance_issue();
     }
     // Move the consume cursor on.
     const TileInfo done = cur;
