@@ -244,6 +244,19 @@ int launch_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32
 // Row movement.  One block per token row; 16-byte accesses when H % 8 == 0.
 // ---------------------------------------------------------------------------
 
+// Launch LAUNCH(KC) with KC = K for the common top-k values, else KC = 0 (the
+// kernel's generic path, K read at run time).
+#define PMX_DISPATCH_K(K, LAUNCH) \
+  switch (K) {                    \
+    case 1: LAUNCH(1); break;     \
+    case 2: LAUNCH(2); break;     \
+    case 4: LAUNCH(4); break;     \
+    case 8: LAUNCH(8); break;     \
+    default: LAUNCH(0); break;    \
+  }
+
+// One thread per 16-byte chunk of a row, whole waves, at most 256 threads:
+// short blocks keep many rows in flight per CU.
 inline unsigned row_threads(int64_t H) {
   int64_t v = (H + 7) / 8;
   v = (v + 63) / 64 * 64;
@@ -274,14 +287,39 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const bf16_t* __restr
 }
 
 // out[t] = bf16( sum_k fp32(term_k) ), term_k = Y[pos] or bf16(Y[pos] * w).
-template <bool VEC, bool WEIGHTED>
+// KC > 0: K == KC at compile time; the K row loads of a chunk are issued
+// together, then summed in k order (the same order as the generic path).
+template <bool VEC, bool WEIGHTED, int KC = 0>
 __global__ __launch_bounds__(256) void gather_rows_kernel(const bf16_t* __restrict__ Y,
-                                                          const int32_t* __restrict__ pos,
-                                                          const bf16_t* __restrict__ w, int32_t K,
-                                                          int64_t H, bf16_t* __restrict__ out) {
+                                                           const int32_t* __restrict__ pos,
+                                                           const bf16_t* __restrict__ w, int32_t K,
+                                                           int64_t H, bf16_t* __restrict__ out) {
   const int64_t t = blockIdx.x;
   const int32_t* p = pos + t * K;
-  if (VEC) {
+  if constexpr (VEC && KC > 0) {
+    const int64_t n8 = H / 8;
+    int64_t rows[KC];
+    float wk[KC];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      rows[k] = (int64_t)p[k] * H;
+      wk[k] = WEIGHTED ? bf16_to_f32(w[t * KC + k]) : 1.f;
+    }
+    for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
+      uint4 v[KC];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) v[k] = reinterpret_cast<const uint4*>(Y + rows[k])[i];
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        float f[8];
+        unpack8(v[k], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += WEIGHTED ? round_bf16(f[j] * wk[k]) : f[j];
+      }
+      reinterpret_cast<uint4*>(out + t * H)[i] = pack8(acc);
+    }
+  } else if (VEC) {
     const int64_t n8 = H / 8;
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -313,20 +351,49 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const bf16_t* __restri
   }
 }
 
-template <bool VEC>
+// KC > 0: K == KC at compile time; a chunk's K loads of Y are issued together.
+template <bool VEC, int KC = 0>
 __global__ __launch_bounds__(256) void combine_bwd_kernel(const bf16_t* __restrict__ dout,
-                                                          const bf16_t* __restrict__ Y,
-                                                          const int32_t* __restrict__ pos,
-                                                          const bf16_t* __restrict__ w, int32_t K,
-                                                          int64_t H, bf16_t* __restrict__ dY,
-                                                          bf16_t* __restrict__ dw) {
+                                                           const bf16_t* __restrict__ Y,
+                                                           const int32_t* __restrict__ pos,
+                                                           const bf16_t* __restrict__ w, int32_t K,
+                                                           int64_t H, bf16_t* __restrict__ dY,
+                                                           bf16_t* __restrict__ dw) {
   __shared__ float red[4][kMaxTopK];
   const int64_t t = blockIdx.x;
   const int32_t* p = pos + t * K;
   float part[kMaxTopK];
 #pragma unroll
   for (int k = 0; k < kMaxTopK; ++k) part[k] = 0.f;
-  if (VEC) {
+  if constexpr (VEC && KC > 0) {
+    const int64_t n8 = H / 8;
+    int64_t rows[KC];
+    float wk[KC];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      rows[k] = (int64_t)p[k] * H;
+      wk[k] = bf16_to_f32(w[t * KC + k]);
+    }
+    for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
+      float d[8];
+      unpack8(reinterpret_cast<const uint4*>(dout + t * H)[i], d);
+      uint4 yv[KC];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) yv[k] = reinterpret_cast<const uint4*>(Y + rows[k])[i];
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        float g[8], y[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) g[j] = d[j] * wk[k];
+        reinterpret_cast<uint4*>(dY + rows[k])[i] = pack8(g);
+        unpack8(yv[k], y);
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += round_bf16(d[j] * y[j]);
+        part[k] += s;
+      }
+    }
+  } else if (VEC) {
     const int64_t n8 = H / 8;
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       float d[8];
@@ -477,8 +544,11 @@ int pmx_moe_gather(const void* Y, const int32_t* pos, int64_t T, int32_t K, int6
   if (!Y || !pos || !out) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
   if (H % 8 == 0 && aligned16(Y) && aligned16(out)) {
-    gather_rows_kernel<true, false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, nullptr, K, H,
-                                                                   (bf16_t*)out);
+#define PMX_GATHER(KC)                                                                                  \
+  gather_rows_kernel<true, false, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, nullptr, K, H, \
+                                                                     (bf16_t*)out)
+    PMX_DISPATCH_K(K, PMX_GATHER);
+#undef PMX_GATHER
   } else {
     gather_rows_kernel<false, false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, nullptr, K, H,
                                                                     (bf16_t*)out);
@@ -494,8 +564,11 @@ int pmx_combine_fwd(const void* Y, const int32_t* pos, const void* w, int64_t T,
   if (!Y || !pos || !w || !out) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
   if (H % 8 == 0 && aligned16(Y) && aligned16(out)) {
-    gather_rows_kernel<true, true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, (const bf16_t*)w,
-                                                                  K, H, (bf16_t*)out);
+#define PMX_COMBINE(KC)                                                                               \
+  gather_rows_kernel<true, true, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, (const bf16_t*)w, \
+                                                                    K, H, (bf16_t*)out)
+    PMX_DISPATCH_K(K, PMX_COMBINE);
+#undef PMX_COMBINE
   } else {
     gather_rows_kernel<false, true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, (const bf16_t*)w,
                                                                    K, H, (bf16_t*)out);
@@ -512,9 +585,11 @@ int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const v
   if (!dout || !Y || !pos || !w || !dY || !dw) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
   if (H % 8 == 0 && aligned16(dout) && aligned16(Y) && aligned16(dY)) {
-    combine_bwd_kernel<true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos,
-                                                            (const bf16_t*)w, K, H, (bf16_t*)dY,
-                                                            (bf16_t*)dw);
+#define PMX_COMBINE_BWD(KC)                                                                            \
+  combine_bwd_kernel<true, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos, \
+                                                              (const bf16_t*)w, K, H, (bf16_t*)dY, (bf16_t*)dw)
+    PMX_DISPATCH_K(K, PMX_COMBINE_BWD);
+#undef PMX_COMBINE_BWD
   } else {
     combine_bwd_kernel<false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos,
                                                              (const bf16_t*)w, K, H, (bf16_t*)dY,
