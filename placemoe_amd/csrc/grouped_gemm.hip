@@ -9,25 +9,27 @@
 // one block per CU walks a tile list derived on the device from `offsets`,
 // so empty groups cost nothing and the host never reads the counts.
 //
-// Block tile 256 x 256, K in steps of 32; 4 waves in a 2x2 arrangement, each
-// owning 128 x 128 of the output as 4 x 4 tiles of v_mfma_f32_32x32x16_bf16
-// whose fp32 accumulators fill the 256 AGPRs.
+// Block tile 256 x 256, K in steps of 64; 8 waves (two per SIMD) in a 2 x 4
+// arrangement, each owning 128 x 64 of the output as 4 x 2 tiles of
+// v_mfma_f32_32x32x16_bf16 with fp32 accumulators: while one wave of a SIMD
+// waits for LDS, a load or the barrier, the other keeps the matrix core busy.
 //
 // Operands stream HBM -> LDS with buffer_load ... lds (no VGPR staging)
-// through four 32 KB stages, three K-tiles in flight while one is multiplied;
-// a block walks its tiles as one stream of K-tiles, so the next tile's first
-// loads overlap the current tile's end and epilogue.  The loads are issued as
-// inline asm, one per pinned group of two MFMAs and one fragment read, and
-// waited for by hand (vmcnt).  Rows or columns outside a group, outside N/M,
-// or past K are masked by buffer range checks (an out-of-range offset loads
-// zeros).
+// through two 64 KB stages: K-tile p+1 lands in one stage while K-tile p is
+// multiplied from the other.  64-deep K-tiles make every row segment a load
+// instruction fetches one whole 128-byte line.  A block walks its tiles as one
+// stream of K-tiles, so the next tile's first loads overlap the current
+// tile's end and epilogue.  The loads are issued as inline asm, one every
+// other pinned MFMA group of the first two k-steps, and waited for by hand
+// (vmcnt).  Rows or columns outside a group, outside N/M, or past K are
+// masked by buffer range checks (an out-of-range offset loads zeros).
 //
 // LDS layouts, both XOR-swizzled in 16-byte chunks so that the fragment reads
 // are free of bank conflicts:
-//   K-contiguous operands (activation rows, fc1/fc2 weights): [row][32 k],
-//     64-byte rows, chunk c stored at c ^ ((row >> 2) & 3); fragments
+//   K-contiguous operands (activation rows, fc1/fc2 weights): [row][64 k],
+//     128-byte rows, chunk c stored at c ^ ((row >> 1) & 7); fragments
 //     are ds_read_b128.
-//   M/N-contiguous operands (dgrad weights, both wgrad operands): [32 k][W],
+//   M/N-contiguous operands (dgrad weights, both wgrad operands): [64 k][W],
 //     chunk c of k-row kk stored at c ^ 4*(kk & 3); fragments are pairs of
 //     ds_read_b64_tr_b16, which transpose 4x16 blocks on the way out of LDS.
 
@@ -35,12 +37,23 @@
 
 namespace {
 
-constexpr int BN = 256, BK = 32;
-// Pipeline stages of (BM + BN) x 32 bf16 that fit next to the group prefix
-// in 160 KB of LDS: 6 x 24 KB for 128-row tiles, 4 x 32 KB for 256-row tiles.
-template <int BM>
-constexpr int nstage() { return BM == 128 ? 6 : 4; }
-constexpr int NTHREADS = 256;
+// K-tiles are 64 deep so that every K-contiguous row segment a load
+// instruction fetches is one whole 128-byte line: with 32-deep K-tiles each
+// segment is half a line, the L1 issues twice the requests to L2 for the
+// same bytes and the texture unit backs up behind it.
+constexpr int BN = 256, BK = 64;
+// Two pipeline stages of (BM + BN) x 64 bf16 (64 KB each) next to the
+// per-wave epilogue regions and the group prefix in 160 KB of LDS.
+constexpr int NSTAGE = 2;
+// Eight waves, two per SIMD, in a 2 x 4 arrangement: each owns 128 x 64 of
+// the output as 4 x 2 tiles of v_mfma_f32_32x32x16_bf16 (128 AGPRs), so that
+// while one wave of a SIMD waits (for LDS, a load or the barrier) the other
+// keeps the matrix core busy.
+constexpr int NWAVES = 8, WAVES_N = 4;
+constexpr int NTHREADS = 64 * NWAVES;
+constexpr int WROWS = 128, WCOLS = 64;  // output tile of one wave
+constexpr int MT = WROWS / 32, NTT = WCOLS / 32;
+constexpr int EPI_BYTES = 16 * WCOLS * 2;  // per wave: 16 output rows
 constexpr int kMaxGroups = 2048;
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always fails the range check
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
@@ -84,13 +97,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, (int)kRsrcWord3);
 }
 
-__device__ __forceinline__ int kc_swz(int row) { return (row >> 2) & 3; }
+// 16-byte chunk swizzle of the 128-byte rows of K-contiguous tiles: 16
+// consecutive rows read at one logical chunk hit 16 distinct (row parity,
+// chunk) bank groups.
+__device__ __forceinline__ int kc_swz(int row) { return (row >> 1) & 7; }
 
 // Per-tile operand description.  Each DMA instruction of this wave has a
 // tile-invariant per-lane byte offset `voff[q0]` (kOOB where the lane's chunk
 // lies outside the operand); the K-tile advance goes into the scalar offset.
-// K-contiguous operands whose K is not a multiple of 32 use `voff_tail` in
-// their last K-tile, which masks the chunks past K.
+// Operands whose K is not a multiple of 64 mask, in their last K-tile, the
+// lanes whose bit in `tmask` is clear (their chunk or k-row lies past K).
 //
 // Per K-tile a wave only adds to the scalar offset (and, for wgrad operands,
 // rebases one descriptor): every per-tile quantity is set up once per tile.
@@ -104,8 +120,13 @@ struct Operand {
   uint32_t split_bytes;           // split * ldb
   int32_t ktail;                  // the partial last K-tile, -1 if none
   uint32_t voff[4];
-  uint32_t voff_tail[4];          // voff with the lanes past K masked (K-tile ktail)
+  uint32_t tmask;                 // bit q0: instruction q0's lane lies within K in K-tile ktail
 };
+
+// The per-lane offset of instruction q0, masked past K in the tail K-tile.
+__device__ __forceinline__ uint32_t lane_off(const Operand& op, int q0, bool tail) {
+  return (tail && !((op.tmask >> q0) & 1u)) ? kOOB : op.voff[q0];
+}
 
 // Where one output tile lies: group, m/n tile, its rows (ragged kinds: the
 // tile's first row and the group's end), and its K-tile count.
@@ -144,13 +165,17 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* dst, uint3
 // An empty descriptor: every offset fails its range check and loads zeros.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t empty_rsrc(const void* base) { return make_rsrc(base, 0); }
 
-// K-contiguous operand, R rows x 32 k: the wave issues R/64 instructions of
-// 16 rows x 64 bytes.  Lane i of instruction q fills row 16q + i/4, physical
-// chunk i%4, i.e. logical chunk (i%4) ^ swz(row).
-// FC1's virtual B rows alternate 64 gate rows (r0) and 64 up rows (r1), so
-// instruction q0 (rows 64*q0 .. 64*q0+63 over the four waves) reads up rows
-// exactly when q0 is odd.
-template <int R, bool SPLIT_ROWS, int Q0B = 0, int Q0E = R / 64>
+// Per wave, the buffer->LDS instructions that bring in an R-row (or R-wide)
+// operand tile of one K-tile: R x 64 bf16 in 1 KB instructions.
+template <int R>
+constexpr int loads_per_wave() { return R * BK * 2 / 1024 / NWAVES; }
+
+// K-contiguous operand, R rows x 64 k: instruction q = q0*NWAVES + wave
+// covers 8 rows x 128 bytes.  Lane i of instruction q fills row 8q + i/8,
+// physical chunk i%8, i.e. logical chunk (i%8) ^ swz(row).
+// FC1's virtual B rows alternate 32 gate rows (r0) and 32 up rows (r1), so
+// instruction q reads up rows exactly when bit 2 of q is set.
+template <int R, bool SPLIT_ROWS, int Q0B = 0, int Q0E = loads_per_wave<R>()>
 __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
   const uint32_t soff = live ? (uint32_t)kt * (BK * 2) : 0u;
   const bool tail = kt == op.ktail;
@@ -159,19 +184,19 @@ __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt,
   const __amdgpu_buffer_rsrc_t r1 = live ? op.r1 : none;
 #pragma unroll
   for (int q0 = Q0B; q0 < Q0E; ++q0) {
-    const int q = q0 * 4 + wave;
-    dma16((SPLIT_ROWS && (q0 & 1)) ? r1 : r0, lds + q * 1024, tail ? op.voff_tail[q0] : op.voff[q0], soff);
+    const int q = q0 * NWAVES + wave;
+    dma16((SPLIT_ROWS && ((q >> 2) & 1)) ? r1 : r0, lds + q * 1024, lane_off(op, q0, tail), soff);
   }
 }
 
-// M/N-contiguous operand, 32 k-rows x W columns: the wave issues W/64
-// instructions of 512/W k-rows x 2W bytes.  Lane i of instruction q fills
+// M/N-contiguous operand, 64 k-rows x W columns: instruction q = q0*NWAVES
+// + wave covers 512/W k-rows x 2W bytes.  Lane i of instruction q fills
 // k-row q*ROWS + i/CH, physical chunk i%CH = logical chunk ^ 4*(kk&3).
 // REBASE (wgrad): the descriptor starts at the K-tile's first row and ends
 // with the group, so rows past the group load zeros.  Otherwise (dgrad
 // weights) the K-tile advance is a scalar offset into r0 (k-rows below split)
 // or r1, and the lanes past K are masked in the last K-tile.
-template <int W, bool REBASE, int Q0B = 0, int Q0E = W / 64>
+template <int W, bool REBASE, int Q0B = 0, int Q0E = loads_per_wave<W>()>
 __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
   constexpr int ROWS = 1024 / (2 * W);
   if constexpr (REBASE) {
@@ -181,7 +206,7 @@ __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt,
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const void*>(uni64((int64_t)base)), uni(bytes));
 #pragma unroll
     for (int q0 = Q0B; q0 < Q0E; ++q0) {
-      const int q = q0 * 4 + wave;
+      const int q = q0 * NWAVES + wave;
       dma16(rk, lds + q * 1024, op.voff[q0], 0u);
     }
   } else {
@@ -189,11 +214,11 @@ __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt,
     const __amdgpu_buffer_rsrc_t none = empty_rsrc(op.base);
 #pragma unroll
     for (int q0 = Q0B; q0 < Q0E; ++q0) {
-      const int q = q0 * 4 + wave;
+      const int q = q0 * NWAVES + wave;
       const int32_t k = kt * BK + q * ROWS;  // first k-row of the instruction
       const bool second = k >= op.split;
       const uint32_t soff = live ? (uint32_t)k * op.ldb - (second ? op.split_bytes : 0u) : 0u;
-      dma16(!live ? none : second ? op.r1 : op.r0, lds + q * 1024, tail ? op.voff_tail[q0] : op.voff[q0], soff);
+      dma16(!live ? none : second ? op.r1 : op.r0, lds + q * 1024, lane_off(op, q0, tail), soff);
     }
   }
 }
@@ -205,7 +230,7 @@ __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt,
 template <int KIND, int BM, int PART = 2>
 __device__ __forceinline__ void issue_stage(char* stage, const Tile<KIND, BM>& tc, int32_t kt, bool live, int wave) {
   char* As = stage;
-  char* Bs = stage + BM * 64;
+  char* Bs = stage + BM * BK * 2;
   if constexpr (PART != 1) {
     if constexpr (a_is_mn<KIND>()) dma_mn<BM, true>(As, tc.A, kt, live, wave);
     else dma_kc<BM, false>(As, tc.A, kt, live, wave);
@@ -223,7 +248,7 @@ __device__ __forceinline__ void issue_one(char* stage, const Tile<KIND, BM>& tc,
     if constexpr (a_is_mn<KIND>()) dma_mn<BM, true, Q0, Q0 + 1>(stage, tc.A, kt, live, wave);
     else dma_kc<BM, false, Q0, Q0 + 1>(stage, tc.A, kt, live, wave);
   } else {
-    char* Bs = stage + BM * 64;
+    char* Bs = stage + BM * BK * 2;
     if constexpr (b_is_mn<KIND>()) dma_mn<BN, KIND == KIND_TN, Q0, Q0 + 1>(Bs, tc.B, kt, live, wave);
     else dma_kc<BN, KIND == KIND_FC1, Q0, Q0 + 1>(Bs, tc.B, kt, live, wave);
   }
@@ -233,7 +258,7 @@ __device__ __forceinline__ void issue_one(char* stage, const Tile<KIND, BM>& tc,
 __device__ __forceinline__ bf16x8_t frag_kc(const char* t, int rb, int ks, int lane) {
   const int row = rb + (lane & 31);
   const int chunk = ks * 2 + (lane >> 5);
-  return *reinterpret_cast<const bf16x8_t*>(t + row * 64 + ((chunk ^ kc_swz(row)) << 4));
+  return *reinterpret_cast<const bf16x8_t*>(t + row * (BK * 2) + ((chunk ^ kc_swz(row)) << 4));
 }
 
 // Fragment of an M/N-contiguous tile (W columns): lane l holds column
@@ -258,57 +283,62 @@ __device__ __forceinline__ bf16x8_t frag_mn(const char* t, int cb, int ks, int l
 // The wave's operand fragments of one 16-deep k-step of a stage.
 template <int BM>
 struct Frags {
-  bf16x8_t a[BM / 64], b[4];
+  bf16x8_t a[MT], b[NTT];
 };
 
 template <int KIND, int BM>
 __device__ __forceinline__ void read_frags(const char* stage, int ks, int wm, int wn, int lane, Frags<BM>& f) {
   const char* As = stage;
-  const char* Bs = stage + BM * 64;
+  const char* Bs = stage + BM * BK * 2;
 #pragma unroll
-  for (int mt = 0; mt < BM / 64; ++mt) {
-    const int rb = wm * (BM / 2) + mt * 32;
+  for (int mt = 0; mt < MT; ++mt) {
+    const int rb = wm * WROWS + mt * 32;
     if constexpr (a_is_mn<KIND>()) f.a[mt] = frag_mn<BM>(As, rb, ks, lane);
     else f.a[mt] = frag_kc(As, rb, ks, lane);
   }
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int cb = wn * 128 + nt * 32;
+  for (int nt = 0; nt < NTT; ++nt) {
+    const int cb = wn * WCOLS + nt * 32;
     if constexpr (b_is_mn<KIND>()) f.b[nt] = frag_mn<BN>(Bs, cb, ks, lane);
     else f.b[nt] = frag_kc(Bs, cb, ks, lane);
   }
 }
 
-// Fragment J of a k-step: A fragments 0 .. BM/64-1, then B fragments 0..3.
+// Fragment J of a k-step: A fragments 0 .. MT-1, then B fragments 0 .. NTT-1.
 template <int KIND, int BM, int J>
 __device__ __forceinline__ void read_frag(const char* stage, int ks, int wm, int wn, int lane, Frags<BM>& f) {
-  constexpr int MT = BM / 64;
   if constexpr (J < MT) {
-    const int rb = wm * (BM / 2) + J * 32;
+    const int rb = wm * WROWS + J * 32;
     if constexpr (a_is_mn<KIND>()) f.a[J] = frag_mn<BM>(stage, rb, ks, lane);
     else f.a[J] = frag_kc(stage, rb, ks, lane);
   } else {
-    const char* Bs = stage + BM * 64;
-    const int cb = wn * 128 + (J - MT) * 32;
+    const char* Bs = stage + BM * BK * 2;
+    const int cb = wn * WCOLS + (J - MT) * 32;
     if constexpr (b_is_mn<KIND>()) f.b[J - MT] = frag_mn<BN>(Bs, cb, ks, lane);
     else f.b[J - MT] = frag_kc(Bs, cb, ks, lane);
   }
 }
 
-// MFMAs I .. I+N-1 of a k-step (index mt * 4 + nt).
+// The I-th fragment read of a k-step, in the order the MFMAs (mt-major)
+// consume them: A0, B0 .. B(NTT-1), then A1 .. A(MT-1).  Fragment ids as in
+// read_frag: A fragments 0 .. MT-1, B fragments MT .. MT+NTT-1.
+constexpr int frag_order(int i) { return i == 0 ? 0 : i <= NTT ? MT + i - 1 : i - NTT; }
+
+// MFMAs I .. I+N-1 of a k-step (index mt * NTT + nt).
 template <int BM, int I, int N>
-__device__ __forceinline__ void mma_some(const Frags<BM>& f, f32x16_t (&acc)[BM / 64][4]) {
+__device__ __forceinline__ void mma_some(const Frags<BM>& f, f32x16_t (&acc)[MT][NTT]) {
 #pragma unroll
   for (int x = I; x < I + N; ++x)
-    acc[x / 4][x % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x / 4], f.b[x % 4], acc[x / 4][x % 4], 0, 0, 0);
+    acc[x / NTT][x % NTT] =
+        __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x / NTT], f.b[x % NTT], acc[x / NTT][x % NTT], 0, 0, 0);
 }
 
 template <int BM>
-__device__ __forceinline__ void mma_frags(const Frags<BM>& f, f32x16_t (&acc)[BM / 64][4]) {
+__device__ __forceinline__ void mma_frags(const Frags<BM>& f, f32x16_t (&acc)[MT][NTT]) {
 #pragma unroll
-  for (int mt = 0; mt < BM / 64; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nt = 0; nt < NTT; ++nt)
       acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mt], f.b[nt], acc[mt][nt], 0, 0, 0);
 }
 
@@ -327,11 +357,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 template <int BM>
-__device__ __forceinline__ void zero_acc(f32x16_t (&acc)[BM / 64][4]) {
+__device__ __forceinline__ void zero_acc(f32x16_t (&acc)[MT][NTT]) {
 #pragma unroll
-  for (int mt = 0; mt < BM / 64; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+    for (int nt = 0; nt < NTT; ++nt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
 }
@@ -339,18 +369,17 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[BM / 64][4]) {
 // Output element i of acc[mt][nt] in lane l sits at row
 // (i/4)*8 + (l/32)*4 + i%4, column l%32 of the 32x32 tile.
 //
-// Epilogue: each wave stages its (BM/2) x 128 output tile in rounds of 16
-// rows as bf16 in its own 4 KB of LDS (row-major, 256-byte rows, 16-byte
-// chunks XOR-swizzled by bit 2 of the row so the two half-waves' 2-byte
-// stores use different banks), then reads each round back one 16-byte chunk
-// per lane and writes whole row segments.  A wave's LDS operations complete in
-// order, so a round may overwrite what the previous one read.
-// Each wave stages its epilogue through a quarter of one pipeline stage.
-template <int BM>
-constexpr int stage_region() { return (BM + BN) * 64 / 4; }
+// Epilogue: each wave stages its 128 x 64 output tile in rounds of 16 rows as
+// bf16 in its own 2 KB of LDS (row-major, 128-byte rows, 16-byte chunks
+// XOR-swizzled by bit 2 of the row so the two half-waves' 2-byte stores use
+// different banks), then reads each round back one 16-byte chunk per lane
+// and writes whole row segments.  A wave's LDS operations complete in order,
+// so a round may overwrite what the previous one read.
+
+__device__ __forceinline__ int epi_swz(int row) { return ((row >> 2) & 1) << 2; }
 
 __device__ __forceinline__ int epi_off(int row, int col) {
-  return row * 256 + ((((col >> 3) ^ (((row >> 2) & 1) << 2))) << 4) + (col & 7) * 2;
+  return row * (WCOLS * 2) + (((col >> 3) ^ epi_swz(row)) << 4) + (col & 7) * 2;
 }
 
 // Round r: rows 16r .. 16r+15 of the wave's tile, i.e. acc[r/2][.][8*(r%2) .. +7].
@@ -360,7 +389,7 @@ __device__ __forceinline__ void stage_round(char* region, int lane, int r, int n
   const int rq = (lane >> 5) * 4;
   const int mt = r >> 1, i0 = (r & 1) * 8;
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt)
+  for (int nt = 0; nt < NTT; ++nt)
 #pragma unroll
     for (int ii = 0; ii < 8; ++ii) {
       if (nt * 32 < ncols) {
@@ -371,53 +400,52 @@ __device__ __forceinline__ void stage_round(char* region, int lane, int r, int n
 }
 
 __device__ __forceinline__ uint4 staged_chunk(const char* region, int row, int chunk) {
-  return *reinterpret_cast<const uint4*>(region + row * 256 + ((chunk ^ (((row >> 2) & 1) << 2)) << 4));
+  return *reinterpret_cast<const uint4*>(region + row * (WCOLS * 2) + ((chunk ^ epi_swz(row)) << 4));
 }
 
 template <int KIND, int BM>
 __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti, int wm, int wn, int lane,
-                                         const f32x16_t (&acc)[BM / 64][4], char* region) {
-  constexpr int WM = BM / 2;
+                                         const f32x16_t (&acc)[MT][NTT], char* region) {
   // The lane index passes through an opaque move so that the epilogue's
   // per-lane address arithmetic stays here instead of being hoisted out of
   // the tile loop, where it would hold registers through every K step.
   asm volatile("" : "+v"(lane));
-  const int cc = lane & 15;  // read-back chunk (8 columns) of the 128-column tile
-  static_for<0, WM / 16>([&](auto round) {
+  const int cc = lane & 7;  // read-back chunk (8 columns) of the 64-column tile
+  static_for<0, WROWS / 16>([&](auto round) {
     constexpr int r = decltype(round)::value;
-    const int64_t rb = wm * WM + r * 16;  // first row of the round within the tile
+    const int64_t rb = wm * WROWS + r * 16;  // first row of the round within the tile
     if constexpr (KIND == KIND_FC1) {
-      // gate | up columns (bf16 GEMM outputs), then act = bf16(bf16(silu(gate)) * up)
+      // The wave's 64 columns are 32 gate and the matching 32 up columns:
+      // first both as bf16 GEMM outputs (gu), then act = bf16(bf16(silu(gate)) * up).
       const int64_t I = P.I;
-      const int64_t j0 = (int64_t)ti.ntile * 128 + wn * 64;
-      stage_round(region, lane, r, 128, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int rl = (lane >> 4) + 4 * q;
-        const int64_t row = ti.row0 + rb + rl;
-        const uint4 v = staged_chunk(region, rl, cc);
-        const int64_t j = j0 + (cc & 7) * 8;
-        if (row < ti.row_end && j < I) *reinterpret_cast<uint4*>(P.gu + row * 2 * I + (cc < 8 ? 0 : I) + j) = v;
-      }
-      stage_round(region, lane, r, 64, [&](int mt, int nt, int i) {
-        const float gb = round_bf16(acc[mt][nt][i]);
-        const float ub = round_bf16(acc[mt][nt + 2][i]);
-        return round_bf16(silu_f32(gb)) * ub;
-      });
+      const int64_t j0 = (int64_t)ti.ntile * 128 + wn * 32;
+      stage_round(region, lane, r, 64, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        const int rl = (lane >> 3) + 8 * q, c8 = lane & 7;
+        const int rl = (lane >> 3) + 8 * q;
         const int64_t row = ti.row0 + rb + rl;
-        const uint4 v = staged_chunk(region, rl, c8);
-        const int64_t j = j0 + c8 * 8;
+        const uint4 v = staged_chunk(region, rl, cc);
+        const int64_t j = j0 + (cc & 3) * 8;
+        if (row < ti.row_end && j < I) *reinterpret_cast<uint4*>(P.gu + row * 2 * I + (cc < 4 ? 0 : I) + j) = v;
+      }
+      stage_round(region, lane, r, 32, [&](int mt, int nt, int i) {
+        const float gb = round_bf16(acc[mt][0][i]);
+        const float ub = round_bf16(acc[mt][1][i]);
+        return round_bf16(silu_f32(gb)) * ub;
+      });
+      {
+        const int rl = lane >> 2, c4 = lane & 3;
+        const int64_t row = ti.row0 + rb + rl;
+        const uint4 v = staged_chunk(region, rl, c4);
+        const int64_t j = j0 + c4 * 8;
         if (row < ti.row_end && j < I) *reinterpret_cast<uint4*>(P.act + row * I + j) = v;
       }
     } else {
-      stage_round(region, lane, r, 128, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
-      const int64_t col = (int64_t)ti.ntile * BN + wn * 128 + cc * 8;
+      stage_round(region, lane, r, 64, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      const int64_t col = (int64_t)ti.ntile * BN + wn * WCOLS + cc * 8;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int rl = (lane >> 4) + 4 * q;
+      for (int q = 0; q < 2; ++q) {
+        const int rl = (lane >> 3) + 8 * q;
         const uint4 v = staged_chunk(region, rl, cc);
         if constexpr (KIND == KIND_TN) {
           const int64_t m = (int64_t)ti.mtile * BM + rb + rl;
@@ -449,34 +477,36 @@ template <int R>
 __device__ __forceinline__ void kc_offsets(Operand& op, int wave, int lane, int64_t K) {
   int32_t krem;
   k_tail(K, op.ktail, krem);
+  op.tmask = 0;
 #pragma unroll
-  for (int q0 = 0; q0 < R / 64; ++q0) {
-    const int row = (q0 * 4 + wave) * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ kc_swz(row);
+  for (int q0 = 0; q0 < loads_per_wave<R>(); ++q0) {
+    const int row = (q0 * NWAVES + wave) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ kc_swz(row);
     op.voff[q0] = (uint32_t)row * op.ldb + (uint32_t)c * 16u;
-    op.voff_tail[q0] = c * 8 < krem ? op.voff[q0] : kOOB;
+    op.tmask |= (c * 8 < krem ? 1u : 0u) << q0;
   }
 }
 
 // Per-lane offsets of an M/N-contiguous operand, relative to the first k-row
 // of each instruction (REBASE: of the K-tile), columns col0.. of the tile.
-// Not REBASE: voff_tail also masks the k-rows past K of the last K-tile.
+// Not REBASE: tmask also masks the k-rows past K of the last K-tile.
 template <int W, bool REBASE>
 __device__ __forceinline__ void mn_offsets(Operand& op, int wave, int lane, int64_t col0, int64_t ncols, int64_t K) {
   constexpr int CH = W / 8, ROWS = 1024 / (2 * W);
   int32_t krem = BK;
   op.ktail = -1;
   if constexpr (!REBASE) k_tail(K, op.ktail, krem);
+  op.tmask = 0;
 #pragma unroll
-  for (int q0 = 0; q0 < W / 64; ++q0) {
-    const int q = q0 * 4 + wave;
+  for (int q0 = 0; q0 < loads_per_wave<W>(); ++q0) {
+    const int q = q0 * NWAVES + wave;
     const int kk = lane / CH;  // k-row within the instruction
     const int krow = q * ROWS + kk;
     const int c = (lane % CH) ^ (4 * (krow & 3));
     const int64_t col = col0 + c * 8;
     const uint32_t r = REBASE ? krow : kk;
     op.voff[q0] = col < ncols ? r * op.ldb + (uint32_t)col * 2u : kOOB;
-    op.voff_tail[q0] = krow < krem ? op.voff[q0] : kOOB;
+    op.tmask |= (krow < krem ? 1u : 0u) << q0;
   }
 }
 
@@ -508,20 +538,21 @@ __device__ __forceinline__ void setup_operands(const GemmParams& P, Tile<KIND, B
     const bf16_t* b1 = P.b.p1 + (int64_t)ti.g * P.b.gs1;
     tc.B.base = reinterpret_cast<const char*>(b0);
     if constexpr (KIND == KIND_FC1) {
-      // virtual B rows: per 128 rows, 64 gate rows (r0) then 64 up rows (r1)
+      // virtual B rows: per 64 rows, 32 gate rows (r0) then 32 up rows (r1)
       tc.B.r0 = make_rsrc(b0, (uint64_t)P.I * P.K * 2);
       tc.B.r1 = make_rsrc(b1, (uint64_t)P.I * P.K * 2);
       tc.B.ldb = (uint32_t)(P.K * 2);
       int32_t krem;
       k_tail(P.K, tc.B.ktail, krem);
       const int64_t j0 = (int64_t)ti.ntile * 128;
+      tc.B.tmask = 0;
 #pragma unroll
-      for (int q0 = 0; q0 < BN / 64; ++q0) {
-        const int row = (q0 * 4 + wave) * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ kc_swz(row);
-        const int64_t j = j0 + (row >> 7) * 64 + (row & 63);
+      for (int q0 = 0; q0 < loads_per_wave<BN>(); ++q0) {
+        const int row = (q0 * NWAVES + wave) * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ kc_swz(row);
+        const int64_t j = j0 + (row >> 6) * 32 + (row & 31);
         tc.B.voff[q0] = j < P.I ? (uint32_t)j * tc.B.ldb + (uint32_t)c * 16u : kOOB;
-        tc.B.voff_tail[q0] = c * 8 < krem ? tc.B.voff[q0] : kOOB;
+        tc.B.tmask |= (c * 8 < krem ? 1u : 0u) << q0;
       }
     } else if constexpr (KIND == KIND_NT) {
       // rows n of B[g] ([N][K]) from row ntile*BN on
@@ -641,37 +672,35 @@ __device__ __forceinline__ void block_barrier() {
 }
 
 // One block per CU walks its tiles (slot, slot + grid, ...) as one stream of
-// K-tiles: the issue cursor runs AHEAD = NSTAGE - 1 K-tiles in front of the
-// multiply, into the next tile, so a tile's first loads are in flight while
-// the previous tile is finished and written out.
+// 64-deep K-tiles through two LDS stages: K-tile p of the stream is
+// multiplied from one stage while K-tile p+1 lands in the other.
 //
-// K-tile number p of the stream lives in stage p % NSTAGE.  Between barrier
-// p-1 (after which stream tile p is in LDS) and barrier p, a wave
-//   - refills the stage of stream tile p-1 with tile p+AHEAD: every wave's
-//     reads of p-1 returned before barrier p-1 (each barrier waits for the
-//     wave's LDS reads too; they were issued under 16 MFMAs, so little waits),
-//   - reads tile p's k-step 0 fragments while it multiplies k-step 1 of tile
-//     p-1, then tile p's k-step 1 fragments while it multiplies k-step 0 of
-//     tile p, so LDS latency hides behind MFMAs,
-//   - waits for its loads of stream tile p+1 (p+2 .. p+AHEAD stay in flight).
-// After an output tile's last K-tile the waves finish it and write it out
-// through that K-tile's stage (its reads are done), then pass one more
-// barrier before that stage is refilled.
+// Between barrier p-1 (after which stream K-tile p is in LDS and every wave
+// has finished reading K-tile p-1) and barrier p, a wave
+//   - issues its loads of K-tile p+1 into the stage of K-tile p-1, one per
+//     MFMA pair of the first two k-steps, so that they have the rest of the
+//     K-tile to land,
+//   - multiplies the four 16-deep k-steps, reading each k-step's fragments
+//     during the previous k-step's MFMAs (k-step 0's during k-step 3 of
+//     K-tile p-1), so that LDS latency hides behind MFMAs,
+//   - waits for its loads and its LDS reads, then passes barrier p.
+// At the end of an output tile the next stream K-tile is issued into the
+// stage just freed before the tile's last k-step is multiplied and the tile
+// is written out (through per-wave epilogue regions outside the stages), so
+// the loads stay in flight across the epilogue.
 template <int KIND, int BM>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P) {
-  constexpr int STAGE_BYTES = (BM + BN) * 64;
-  constexpr int PER_STAGE = (BM + BN) / 64;  // DMA instructions per wave per stage
-  constexpr int NSTAGE = nstage<BM>();
-  constexpr int AHEAD = NSTAGE - 1;
-  constexpr int REGION = stage_region<BM>();
-  static_assert(REGION >= 16 * 256, "an epilogue round stages 16 rows of 256 bytes");
+  static_assert(BM == 256, "the schedule below is written for 256 x 256 tiles");
+  constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
+  constexpr int QA = loads_per_wave<BM>(), QB = loads_per_wave<BN>();  // per wave and K-tile
   __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char epi[NWAVES * EPI_BYTES];
   __shared__ int32_t tpre[kMaxGroups + 1];
   __shared__ int32_t scan_buf[NTHREADS];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = uni(t >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int G = P.G;
 
   int64_t ntn, tiles_per_group = 0, total;
@@ -682,13 +711,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     total = tiles_per_group * G;
   } else {
     ntn = (KIND == KIND_FC1) ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
-    // Exclusive prefix of m-tiles per group: 8 groups per thread, then a
-    // block scan of the 256 partial sums.
-    int32_t loc[8];
+    // Exclusive prefix of m-tiles per group: GPT groups per thread, then a
+    // block scan of the NTHREADS partial sums.
+    constexpr int GPT = kMaxGroups / NTHREADS;
+    int32_t loc[GPT];
     int32_t sum = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int g = t * 8 + i;
+    for (int i = 0; i < GPT; ++i) {
+      const int g = t * GPT + i;
       int32_t v = 0;
       if (g < G) v = (P.offsets[g + 1] - P.offsets[g] + BM - 1) / BM;
       loc[i] = sum;
@@ -704,8 +734,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     }
     const int32_t base = scan_buf[t] - sum;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int g = t * 8 + i;
+    for (int i = 0; i < GPT; ++i) {
+      const int g = t * GPT + i;
       if (g < G) tpre[g] = base + loc[i];
     }
     if (t == NTHREADS - 1) tpre[G] = scan_buf[NTHREADS - 1];
@@ -730,7 +760,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     zero_tile<BM>(P, cur, t);
   }
 
-  // Issue cursor: AHEAD K-tiles in front, over the same tile sequence.
+  // Issue cursor: one K-tile in front, over the same tile sequence.  Past the
+  // block's last K-tile it issues through an empty descriptor (zeros).
   Tile<KIND, BM> it;
   int64_t i_tile = c_tile;
   int32_t i_kt = 0;
@@ -754,50 +785,82 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     advance_issue();
   };
 
-#pragma unroll
-  for (int p = 0; p < AHEAD; ++p) issue_next(lds + p * STAGE_BYTES);
-  wait_loads<(AHEAD - 1) * PER_STAGE>();
+  // Prologue: the first K-tile lands in stage 0, then the second is issued.
+  issue_next(lds);
+  wait_loads<0>();
   block_barrier();
+  int cs = 0;  // stage of the K-tile being multiplied
+  issue_next(lds + STAGE_BYTES);
 
-  f32x16_t acc[BM / 64][4];
+  // Per k-step: NM MFMAs, one per pinned group, and NR fragment reads, two
+  // per group in the first groups.  The next K-tile's QA + QB loads go one
+  // every other group of the first two k-steps.
+  constexpr int NM = MT * NTT, NR = MT + NTT, PER = 1, NF = NM;
+  static_assert(NR % 2 == 0 && NR / 2 <= NF && QA + QB == NF, "schedule shape");
+  f32x16_t acc[MT][NTT];
   Frags<BM> f0, f1;
-  int cs = 0;  // stage of the stream K-tile being multiplied
-  auto next_stage = [](int c) { return c + 1 == NSTAGE ? 0 : c + 1; };
-  auto refill_stage = [](int c) { return c + AHEAD >= NSTAGE ? c + AHEAD - NSTAGE : c + AHEAD; };
+
+  // The fragment reads of k-step KS into f: two per MFMA group in the first
+  // half of the groups, in the order the MFMAs consume them.
+  auto reads_half = [&](auto jj, const char* stage, auto ks, Frags<BM>& f) __attribute__((always_inline)) {
+    constexpr int j = decltype(jj)::value;
+    if constexpr (2 * j < NR) {
+      read_frag<KIND, BM, frag_order(2 * j)>(stage, decltype(ks)::value, wm, wn, lane, f);
+      read_frag<KIND, BM, frag_order(2 * j + 1)>(stage, decltype(ks)::value, wm, wn, lane, f);
+    }
+  };
+  // k-step KS of the current K-tile: MFMAs of k-step KS-1 (fragments `fm`)
+  // interleaved with the reads of k-step KS into `fr`, and, with LOADS, the
+  // loads of the next K-tile that fall into this k-step's groups.
+  auto kstep = [&](auto ks, auto loads, auto oper, const char* stage, char* refill, const Frags<BM>& fm,
+                   Frags<BM>& fr) __attribute__((always_inline)) {
+    static_for<0, NF>([&](auto jj) __attribute__((always_inline)) {
+      constexpr int j = decltype(jj)::value;
+      if constexpr (decltype(loads)::value) {
+        static_for<0, QA + QB>([&](auto ll) __attribute__((always_inline)) {
+          constexpr int l = decltype(ll)::value;
+          if constexpr (2 * l == decltype(ks)::value * NF + j) {
+            if constexpr (l < QA) issue_one<KIND, BM, 0, l>(refill, it, i_kt, i_live, wave);
+            else issue_one<KIND, BM, 1, l - QA>(refill, it, i_kt, i_live, wave);
+          }
+        });
+      }
+      reads_half(jj, stage, ks, fr);
+      mma_some<BM, j * PER, PER>(fm, acc);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
   for (;;) {
-    // Output tile `cur`; its first K-tile is in stage cs and in LDS.
+    // Output tile `cur`: its first K-tile is in stage cs, and the next stream
+    // K-tile is in flight into the other stage.
     zero_acc<BM>(acc);
-    issue_next(lds + refill_stage(cs) * STAGE_BYTES);
-    read_frags<KIND, BM>(lds + cs * STAGE_BYTES, 0, wm, wn, lane, f0);
-    read_frags<KIND, BM>(lds + cs * STAGE_BYTES, 1, wm, wn, lane, f1);
-    mma_frags<BM>(f0, acc);
-    for (int32_t kt = 1; kt < cur.nk; ++kt) {
-      wait_loads_lds<(AHEAD - 1) * PER_STAGE>();
+    {
+      // K-tile 0: no MFMAs pending, and the next K-tile is already in flight.
+      const char* stage = lds + cs * STAGE_BYTES;
+      char* refill = lds + (cs ^ 1) * STAGE_BYTES;
+      static_for<0, NR>([&](auto jj) __attribute__((always_inline)) {
+        constexpr int j = decltype(jj)::value;
+        read_frag<KIND, BM, frag_order(j)>(stage, 0, wm, wn, lane, f0);
+      });
+      kstep(Int<1>{}, Int<0>{}, Int<0>{}, stage, refill, f0, f1);
+      kstep(Int<2>{}, Int<0>{}, Int<0>{}, stage, refill, f1, f0);
+      kstep(Int<3>{}, Int<0>{}, Int<0>{}, stage, refill, f0, f1);
+      wait_loads_lds<0>();
       block_barrier();
-      cs = next_stage(cs);
-      char* stage = lds + cs * STAGE_BYTES;
-      char* refill = lds + refill_stage(cs) * STAGE_BYTES;
-      // One pinned group per A/B fragment: its load (every other group), the
-      // fragment read for the next k-step, and a slice of this k-step's
-      // MFMAs.  A load whose issue stalls in the texture unit then stalls
-      // while MFMAs run, instead of holding back a burst of them.
-      constexpr int NF = BM / 64 + 4, NM = (BM / 64) * 4, PER = NM / NF;
-      static_assert(NM % NF == 0 && NF % 2 == 0 && PER_STAGE == NF, "schedule shape");
-      static_for<0, NF>([&](auto jj) {
-        constexpr int j = decltype(jj)::value;
-        if constexpr (j % 2 == 0) issue_one<KIND, BM, 0, j / 2>(refill, it, i_kt, i_live, wave);
-        read_frag<KIND, BM, j>(stage, 0, wm, wn, lane, f0);
-        mma_some<BM, j * PER, PER>(f1, acc);
-        __builtin_amdgcn_sched_barrier(0);
-      });
-      static_for<0, NF>([&](auto jj) {
-        constexpr int j = decltype(jj)::value;
-        if constexpr (j % 2 == 0) issue_one<KIND, BM, 1, j / 2>(refill, it, i_kt, i_live, wave);
-        read_frag<KIND, BM, j>(stage, 1, wm, wn, lane, f1);
-        mma_some<BM, j * PER, PER>(f0, acc);
-        __builtin_amdgcn_sched_barrier(0);
-      });
+      cs ^= 1;
+    }
+    for (int32_t kt = 1; kt < cur.nk; ++kt) {
+      const char* stage = lds + cs * STAGE_BYTES;
+      char* refill = lds + (cs ^ 1) * STAGE_BYTES;
+      kstep(Int<0>{}, Int<1>{}, Int<0>{}, stage, refill, f1, f0);
+      kstep(Int<1>{}, Int<1>{}, Int<0>{}, stage, refill, f0, f1);
+      kstep(Int<2>{}, Int<1>{}, Int<0>{}, stage, refill, f1, f0);
+      kstep(Int<3>{}, Int<1>{}, Int<0>{}, stage, refill, f0, f1);
       advance_issue();
+      wait_loads_lds<0>();
+      block_barrier();
+      cs ^= 1;
     }
     // Move the consume cursor on.
     const TileInfo done = cur;
@@ -810,19 +873,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       }
       zero_tile<BM>(P, cur, t);
     }
-    // More tiles: the next tile's first K-tile lands, and every wave's reads
-    // of this tile's last stage have returned, so the epilogue may stage
-    // through that stage while the next AHEAD - 1 K-tiles are in flight.
-    // Last tile: drain the remaining (empty) loads.
-    if (more) wait_loads_lds<(AHEAD - 1) * PER_STAGE>();
-    else wait_loads_lds<0>();
-    block_barrier();
+    // The stage of the tile's last K-tile is free (barrier above): the next
+    // stream K-tile goes there while this tile is finished and written out.
+    issue_next(lds + (cs ^ 1) * STAGE_BYTES);
     mma_frags<BM>(f1, acc);
-    epilogue<KIND, BM>(P, done, wm, wn, lane, acc, lds + cs * STAGE_BYTES + wave * REGION);
-    if (!more) return;
-    // The next step refills this stage: every wave must be done with it.
-    block_barrier();
-    cs = next_stage(cs);
+    epilogue<KIND, BM>(P, done, wm, wn, lane, acc, epi + wave * EPI_BYTES);
+    if (!more) {
+      wait_loads<0>();
+      return;
+    }
   }
 }
 
