@@ -7,7 +7,9 @@ dgrad + SwiGLU backward, fc2 and fc1 wgrad, fc1 dgrad, unpermute gradient).
 Inputs and weights are resident in HBM before the timed region starts.
 
 Default workload: BASELINE config 2 (Qwen3-30B-A3B shape: T=16384, H=2048,
-E=128 -> C=160 copies, top-8, I=768, 8 sources).  ``--config`` picks another.
+E=128 -> C=160 copies, top-8, I=768, 8 sources).  ``--config`` picks another;
+``--config fold`` (config 5) adds the replica-gradient fold of both copy
+gradients (fp32 logical sums, written back to every copy) to each step.
 
 Prints ONE JSON line.  ``value`` is the layer fwd+bwd time in ms (lower is
 better); the grouped-GEMM TFLOP/s and permute GB/s of the same run, the
@@ -54,6 +56,8 @@ STAGES = [
     ("pmx_group_gemm_tn", 1, "fc1_wgrad"),
     ("pmx_group_gemm_nn", 0, "fc1_dgrad"),
     ("pmx_moe_gather", 0, "unpermute_grad"),
+    ("pmx_replica_fold", 0, "fold_gate_up"),
+    ("pmx_replica_fold", 1, "fold_down"),
 ]
 
 
@@ -123,21 +127,33 @@ def cpu_baseline(wl, sample_tokens: int, backward: bool):
         if backward:
             O.moe_layer_backward(dout, fwd, w, fc1, fc2)
 
-    run()  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    ms = float(np.median(times)) * 1e3
-    return {
-        "value": ms * wl.T / Ts,
-        "unit": "ms",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"oracle layer {'fwd+bwd' if backward else 'fwd'} on {Ts} of {wl.T} tokens, median of 3 "
-                  f"({ms:.1f} ms), scaled x{wl.T / Ts:g} to the full batch",
-    }
+    def median_ms(fn):
+        fn()  # warm-up
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times)) * 1e3
+
+    ms = median_ms(run)
+    value = ms * wl.T / Ts
+    sample = (f"oracle layer {'fwd+bwd' if backward else 'fwd'} on {Ts} of {wl.T} tokens, median of 3 "
+              f"({ms:.1f} ms), scaled x{wl.T / Ts:g} to the full batch")
+    if wl.name == "fold":
+        # Replica fold of both copy gradients over the copies of the first
+        # `fold_experts` logical experts, scaled by the copy count.
+        fold_experts = 4
+        L = np.asarray(wl.slot_to_logical)
+        picked = np.nonzero(L < fold_experts)[0]
+        gsub = [torch.randn((picked.size,) + tuple(t.shape[1:]), generator=torch.Generator().manual_seed(2))
+                .to(torch.bfloat16) for t in (fc1, fc2)]
+        fold_ms = median_ms(lambda: [O.replica_fold(g, L[picked], fold_experts) for g in gsub])
+        value += fold_ms * L.size / picked.size
+        sample += (f"; plus the oracle replica fold of both copy gradients over the {picked.size} copies of "
+                   f"{fold_experts} experts ({fold_ms:.1f} ms), scaled x{L.size / picked.size:g} to all "
+                   f"{L.size} copies")
+    return {"value": value, "unit": "ms", "cores": threads, "kind": "port", "sample": sample}
 
 
 def main():
@@ -174,6 +190,15 @@ def main():
     fc2 = wl.fc2.requires_grad_(backward)
     dout = torch.randn((T, H), device=dev, generator=torch.Generator(device=dev).manual_seed(1)).to(torch.bfloat16)
 
+    fold = args.config == "fold"
+    if fold:
+        from placemoe_amd import kernels
+        from placemoe_amd.placement import copy_table
+
+        off_np, slots_np = copy_table(wl.slot_to_logical, wl.num_experts)
+        copy_off = torch.as_tensor(off_np, dtype=torch.int32, device=dev)
+        copy_slots = torch.as_tensor(slots_np, dtype=torch.int32, device=dev)
+
     def step():
         for p in (x, w, fc1, fc2):
             p.grad = None
@@ -181,6 +206,9 @@ def main():
                                    sources=wl.sources)
         if backward:
             out.backward(dout)
+        if fold:
+            for g in (fc1.grad, fc2.grad):
+                kernels.replica_fold(g, copy_off, copy_slots, wl.num_experts, writeback=True)
         return out
 
     for _ in range(args.warmup):
@@ -217,6 +245,10 @@ def main():
     bw = {"permute": work["permute_bytes"], "combine_fwd": work["combine_fwd_bytes"],
           "combine_bwd": work["combine_bwd_bytes"], "unpermute_grad": work["unpermute_grad_bytes"],
           "route": work["route_bytes"]}
+    if fold:
+        # bf16 copy gradients read, fp32 logical sums written, totals written back to every copy
+        for label, per_copy in (("fold_gate_up", 2 * I * H), ("fold_down", H * I)):
+            bw[label] = C * per_copy * 2 + wl.num_experts * per_copy * 4 + C * per_copy * 2
     bandwidth = {k: round(v / (kernels_ms[k] * 1e-3) / 1e9, 1) for k, v in bw.items() if k in kernels_ms}
 
     result = {

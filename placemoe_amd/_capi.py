@@ -11,7 +11,9 @@ import os
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libplacemoe_amd.so"
+# The in-tree build; PLACEMOE_AMD_LIBRARY names another build of the same C ABI.
+_DEFAULT_LIB = Path(__file__).resolve().parent / "_lib" / "libplacemoe_amd.so"
+LIB_PATH = Path(os.environ.get("PLACEMOE_AMD_LIBRARY") or _DEFAULT_LIB)
 
 PMX_OK = 0
 PMX_ERR_HIP = 1

@@ -44,6 +44,25 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return v;
 }
 
+// 16-byte streaming (non-temporal) global load and store, for row data that
+// a kernel touches exactly once.  Measured on the row-movement kernels inside
+// the layer: streaming loads are 5-20% faster than plain loads; streaming
+// stores are faster only where each token writes a single row (top-1), and
+// slower where it writes K > 1 rows, so the kernels choose per call.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_stream(void* p, const uint4 v) {
+  __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(p));
+}
+template <bool STREAM>
+__device__ __forceinline__ void st_row(void* p, const uint4 v) {
+  if constexpr (STREAM) st_stream(p, v);
+  else *reinterpret_cast<uint4*>(p) = v;
+}
+
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + __expf(-x)); }
 

@@ -23,7 +23,7 @@ __global__ __launch_bounds__(256) void replica_fold_kernel(bf16_t* __restrict__ 
       const int64_t c = copy_slots[j];
       if (slot_tokens != nullptr && slot_tokens[c] <= 0) continue;
       float f[8];
-      unpack8(*reinterpret_cast<const uint4*>(grads + c * P + i), f);
+      unpack8(ld_stream(grads + c * P + i), f);
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc[q] += f[q];
     }

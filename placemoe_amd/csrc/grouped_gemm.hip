@@ -898,9 +898,9 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const bf16_t* __restric
     const int64_t c = (int64_t)(e - r * chunks) * 8;
     const int64_t row = (int64_t)r * ld, up = ld / 2;
     float dact[8], g[8], u[8], dgate[8], dup[8];
-    unpack8(*reinterpret_cast<const uint4*>(dg1 + row + up + c), dact);
-    unpack8(*reinterpret_cast<const uint4*>(gu + row + c), g);
-    unpack8(*reinterpret_cast<const uint4*>(gu + row + up + c), u);
+    unpack8(ld_stream(dg1 + row + up + c), dact);
+    unpack8(ld_stream(gu + row + c), g);
+    unpack8(ld_stream(gu + row + up + c), u);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const float s = round_bf16(silu_f32(g[q]));

@@ -256,17 +256,20 @@ int launch_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32
   }
 
 // One thread per 16-byte chunk of a row, whole waves, at most 256 threads:
-// short blocks keep many rows in flight per CU.
+// short blocks keep many rows in flight per CU (measured faster than one
+// thread per chunk of rows up to 7168 bf16 with 1024-thread blocks).
+constexpr int kRowThreads = 256;
 inline unsigned row_threads(int64_t H) {
   int64_t v = (H + 7) / 8;
   v = (v + 63) / 64 * 64;
   if (v < 64) v = 64;
-  if (v > 256) v = 256;
+  if (v > kRowThreads) v = kRowThreads;
   return (unsigned)v;
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(256) void scatter_rows_kernel(const bf16_t* __restrict__ X,
+// STREAM_ST: streaming stores of the copies (top-1 only; see st_row).
+template <bool VEC, bool STREAM_ST = false>
+__global__ __launch_bounds__(kRowThreads) void scatter_rows_kernel(const bf16_t* __restrict__ X,
                                                            const int32_t* __restrict__ pos, int32_t K,
                                                            int64_t H, bf16_t* __restrict__ Xp) {
   const int64_t t = blockIdx.x;
@@ -275,8 +278,8 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const bf16_t* __restr
     const int64_t n8 = H / 8;
     const uint4* src = reinterpret_cast<const uint4*>(X + t * H);
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
-      const uint4 v = src[i];
-      for (int k = 0; k < K; ++k) reinterpret_cast<uint4*>(Xp + (int64_t)p[k] * H)[i] = v;
+      const uint4 v = ld_stream(src + i);
+      for (int k = 0; k < K; ++k) st_row<STREAM_ST>(reinterpret_cast<uint4*>(Xp + (int64_t)p[k] * H) + i, v);
     }
   } else {
     for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
@@ -290,7 +293,7 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const bf16_t* __restr
 // KC > 0: K == KC at compile time; the K row loads of a chunk are issued
 // together, then summed in k order (the same order as the generic path).
 template <bool VEC, bool WEIGHTED, int KC = 0>
-__global__ __launch_bounds__(256) void gather_rows_kernel(const bf16_t* __restrict__ Y,
+__global__ __launch_bounds__(kRowThreads) void gather_rows_kernel(const bf16_t* __restrict__ Y,
                                                            const int32_t* __restrict__ pos,
                                                            const bf16_t* __restrict__ w, int32_t K,
                                                            int64_t H, bf16_t* __restrict__ out) {
@@ -308,7 +311,7 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const bf16_t* __restri
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       uint4 v[KC];
 #pragma unroll
-      for (int k = 0; k < KC; ++k) v[k] = reinterpret_cast<const uint4*>(Y + rows[k])[i];
+      for (int k = 0; k < KC; ++k) v[k] = ld_stream(reinterpret_cast<const uint4*>(Y + rows[k]) + i);
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int k = 0; k < KC; ++k) {
@@ -324,7 +327,7 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const bf16_t* __restri
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       for (int k = 0; k < K; ++k) {
-        const uint4 v = reinterpret_cast<const uint4*>(Y + (int64_t)p[k] * H)[i];
+        const uint4 v = ld_stream(reinterpret_cast<const uint4*>(Y + (int64_t)p[k] * H) + i);
         float f[8];
         unpack8(v, f);
         if (WEIGHTED) {
@@ -352,14 +355,15 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const bf16_t* __restri
 }
 
 // KC > 0: K == KC at compile time; a chunk's K loads of Y are issued together.
+// Top-1 (KC == 1) stores dY with streaming stores (see st_row).
 template <bool VEC, int KC = 0>
-__global__ __launch_bounds__(256) void combine_bwd_kernel(const bf16_t* __restrict__ dout,
+__global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* __restrict__ dout,
                                                            const bf16_t* __restrict__ Y,
                                                            const int32_t* __restrict__ pos,
                                                            const bf16_t* __restrict__ w, int32_t K,
                                                            int64_t H, bf16_t* __restrict__ dY,
                                                            bf16_t* __restrict__ dw) {
-  __shared__ float red[4][kMaxTopK];
+  __shared__ float red[kRowThreads / 64][kMaxTopK];
   const int64_t t = blockIdx.x;
   const int32_t* p = pos + t * K;
   float part[kMaxTopK];
@@ -376,16 +380,16 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const bf16_t* __restri
     }
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       float d[8];
-      unpack8(reinterpret_cast<const uint4*>(dout + t * H)[i], d);
+      unpack8(ld_stream(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
       uint4 yv[KC];
 #pragma unroll
-      for (int k = 0; k < KC; ++k) yv[k] = reinterpret_cast<const uint4*>(Y + rows[k])[i];
+      for (int k = 0; k < KC; ++k) yv[k] = ld_stream(reinterpret_cast<const uint4*>(Y + rows[k]) + i);
 #pragma unroll
       for (int k = 0; k < KC; ++k) {
         float g[8], y[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) g[j] = d[j] * wk[k];
-        reinterpret_cast<uint4*>(dY + rows[k])[i] = pack8(g);
+        st_row<KC == 1>(reinterpret_cast<uint4*>(dY + rows[k]) + i, pack8(g));
         unpack8(yv[k], y);
         float s = 0.f;
 #pragma unroll
@@ -397,7 +401,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const bf16_t* __restri
     const int64_t n8 = H / 8;
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       float d[8];
-      unpack8(reinterpret_cast<const uint4*>(dout + t * H)[i], d);
+      unpack8(ld_stream(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
 #pragma unroll
       for (int k = 0; k < kMaxTopK; ++k) {
         if (k < K) {
@@ -407,7 +411,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const bf16_t* __restri
 #pragma unroll
           for (int j = 0; j < 8; ++j) g[j] = d[j] * wk;
           reinterpret_cast<uint4*>(dY + row * H)[i] = pack8(g);
-          unpack8(reinterpret_cast<const uint4*>(Y + row * H)[i], y);
+          unpack8(ld_stream(reinterpret_cast<const uint4*>(Y + row * H) + i), y);
           float s = 0.f;
 #pragma unroll
           for (int j = 0; j < 8; ++j) s += round_bf16(d[j] * y[j]);
@@ -454,7 +458,7 @@ __global__ void invert_kernel(const int32_t* __restrict__ pos, int64_t N, int32_
 
 // out[r] = sum_{j in [off[r], off[r+1])} src[order[j]]  (fp32, bf16 store).
 template <bool VEC>
-__global__ __launch_bounds__(256) void segment_rows_kernel(const bf16_t* __restrict__ src,
+__global__ __launch_bounds__(kRowThreads) void segment_rows_kernel(const bf16_t* __restrict__ src,
                                                            const int32_t* __restrict__ order,
                                                            const int32_t* __restrict__ off, int64_t H,
                                                            bf16_t* __restrict__ out) {
@@ -466,7 +470,7 @@ __global__ __launch_bounds__(256) void segment_rows_kernel(const bf16_t* __restr
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       for (int32_t j = b; j < e; ++j) {
         float f[8];
-        unpack8(reinterpret_cast<const uint4*>(src + (int64_t)order[j] * H)[i], f);
+        unpack8(ld_stream(reinterpret_cast<const uint4*>(src + (int64_t)order[j] * H) + i), f);
 #pragma unroll
         for (int q = 0; q < 8; ++q) acc[q] += f[q];
       }
@@ -529,7 +533,11 @@ int pmx_moe_scatter(const void* X, const int32_t* pos, int64_t T, int32_t K, int
   if (!X || !pos || !Xp) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
   if (H % 8 == 0 && aligned16(X) && aligned16(Xp)) {
-    scatter_rows_kernel<true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp);
+    if (K == 1) {
+      scatter_rows_kernel<true, true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp);
+    } else {
+      scatter_rows_kernel<true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp);
+    }
   } else {
     scatter_rows_kernel<false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp);
   }
