@@ -189,6 +189,25 @@ int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const int32_t* co
                      const int64_t* slot_tokens, int32_t E, int32_t C, int64_t P, float* out,
                      int32_t writeback, pmx_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Route statistics for the placement planner                               */
+/* ------------------------------------------------------------------------ */
+
+/* Source-conditioned demand and co-selection counts of one routing sample,
+ * added to caller-zeroed int64 tables (so a profiling window accumulates on
+ * the device):
+ *   demand[s,e]     += #{(t,k) : src(t) == s, sel[t,k] == e}
+ *   affinity[s,a,b] += #{(t, k < k') : src(t) == s, {sel[t,k], sel[t,k']} == {a,b}}, a != b
+ * (symmetric, zero diagonal).  sel: int64 [T*K] logical expert ids; src:
+ * int64 [T] source ranks, or NULL for `src_const`; demand [S*E]; affinity
+ * [S*E*E]; K <= 32.  A token with an id outside [0,E) or a source outside
+ * [0,S) is skipped and sets *status (device int32, caller-zeroed) to 1.
+ * Replaces profile_route_statistics
+ * (veomni/distributed/moe/hiermoe/placemoe/statistics.py:30-64). */
+int pmx_route_statistics(const int64_t* sel, const int64_t* src, int32_t src_const, int32_t S,
+                         int32_t E, int64_t T, int32_t K, int64_t* demand, int64_t* affinity,
+                         int32_t* status, pmx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,11 @@ How each function is pinned (the checks live in ``tests/test_oracle_*.py``):
 * ``replica_fold`` - the reference's known answer 10+2=12, 20+3=23
   (tests/distributed/test_hiermoe.py:3286-3338) and "sum of copy grads ==
   logical-expert grad of the eager model" (tests/distributed/test_hiermoe.py:3765-3778).
+* ``route_statistics`` - the reference's known answer (demand
+  [[2,1,1,0],[0,1,1,2]] and the co-selection entries of
+  tests/distributed/test_placemoe_optimizer.py:50-73), a pure-Python count
+  over token pairs on random samples, and the invariants sum(demand[s]) =
+  T_s*K, symmetry, zero diagonal, sum(affinity[s]) = 2 * #distinct pairs.
 """
 
 from __future__ import annotations
@@ -345,3 +350,35 @@ def moe_layer_backward(dout, fwd, w, w1, w2):
     dxp, dw1, dw2, dg1 = expert_layer_backward(dy, fwd["xp"], fwd["gu"], fwd["offsets"], w1, w2)
     dx = unpermute_grad(dxp, fwd["pos"])
     return dict(dy=dy, dw=dw, dxp=dxp, dw1=dw1, dw2=dw2, dg1=dg1, dx=dx)
+
+
+# ---------------------------------------------------------------------------
+# Route statistics for the placement planner
+# ---------------------------------------------------------------------------
+
+
+def route_statistics(samples, num_experts: int):
+    """Source-conditioned demand [S, E] and co-selection affinity [S, E, E]
+    (float64) of routing samples, ``profile_route_statistics``
+    (veomni/distributed/moe/hiermoe/placemoe/statistics.py:30-64): demand is
+    the bincount of each source's routes; every unordered pair of top-k
+    positions adds one to (a, b) and to (b, a); the diagonal is zeroed.
+
+    ``samples``: a list of samples, each a list (one per source rank) of
+    integer arrays [tokens, top_k]."""
+    S = len(samples[0])
+    demand = np.zeros((S, num_experts), dtype=np.float64)
+    affinity = np.zeros((S, num_experts, num_experts), dtype=np.float64)
+    for sample in samples:
+        for s, route in enumerate(sample):
+            route = np.asarray(route, dtype=np.int64)
+            demand[s] += np.bincount(route.reshape(-1), minlength=num_experts)
+            K = route.shape[1]
+            for a in range(K):
+                for b in range(a + 1, K):
+                    pair = route[:, a] * num_experts + route[:, b]
+                    counts = np.bincount(pair, minlength=num_experts * num_experts).reshape(num_experts, num_experts)
+                    affinity[s] += counts + counts.T
+    for m in affinity:
+        np.fill_diagonal(m, 0.0)
+    return demand, affinity

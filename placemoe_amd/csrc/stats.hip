@@ -1,0 +1,64 @@
+// Route statistics for the PlaceMoE planner on gfx950: source-conditioned
+// expert demand and pairwise co-selection counts of a routing sample,
+// accumulated on the device so that a profiling window needs no host copy of
+// the routes.
+//
+// One thread per token.  Counts are exact integers (64-bit device-scope
+// atomics into tables of S*E and S*E*E entries); the tables are small next to
+// the routing tensors and the updates of different tokens rarely collide.
+
+#include "common.h"
+
+namespace {
+
+constexpr int kStatsMaxTopK = 32;
+
+__global__ __launch_bounds__(256) void route_stats_kernel(const int64_t* __restrict__ sel,
+                                                          const int64_t* __restrict__ src, int32_t src_const,
+                                                          int32_t S, int32_t E, int64_t T, int32_t K,
+                                                          unsigned long long* __restrict__ demand,
+                                                          unsigned long long* __restrict__ affinity,
+                                                          int32_t* __restrict__ status) {
+  for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < T; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t s = src != nullptr ? src[t] : (int64_t)src_const;
+    const int64_t* row = sel + t * K;
+    bool ok = s >= 0 && s < S;
+    for (int k = 0; k < K; ++k) ok = ok && row[k] >= 0 && row[k] < E;
+    if (!ok) {
+      // The whole token is skipped; the host reports the sample as invalid.
+      atomicOr(status, 1);
+      continue;
+    }
+    const int64_t base = s * E;
+    for (int k = 0; k < K; ++k) atomicAdd(&demand[base + row[k]], 1ull);
+    // Unordered pairs k < k' of distinct experts, counted in both orders; a
+    // pair of equal experts would land on the diagonal, which stays zero.
+    for (int a = 0; a < K; ++a) {
+      const int64_t ea = row[a];
+      for (int b = a + 1; b < K; ++b) {
+        const int64_t eb = row[b];
+        if (ea == eb) continue;
+        atomicAdd(&affinity[(base + ea) * E + eb], 1ull);
+        atomicAdd(&affinity[(base + eb) * E + ea], 1ull);
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int pmx_route_statistics(const int64_t* sel, const int64_t* src, int32_t src_const, int32_t S,
+                                    int32_t E, int64_t T, int32_t K, int64_t* demand, int64_t* affinity,
+                                    int32_t* status, pmx_stream_t stream) {
+  if (S <= 0 || E <= 0 || T < 0 || K <= 0 || K > kStatsMaxTopK) return PMX_ERR_ARG;
+  if (!demand || !affinity || !status) return PMX_ERR_ARG;
+  if ((int64_t)S * E * E > ((int64_t)1 << 40)) return PMX_ERR_SHAPE;
+  if (T == 0) return PMX_OK;
+  if (!sel) return PMX_ERR_ARG;
+  const int64_t blocks = (T + 255) / 256 < 4096 ? (T + 255) / 256 : 4096;
+  route_stats_kernel<<<(unsigned)blocks, 256, 0, stream>>>(
+      sel, src, src_const, S, E, T, K, reinterpret_cast<unsigned long long*>(demand),
+      reinterpret_cast<unsigned long long*>(affinity), status);
+  PMX_LAUNCH_CHECK();
+  return PMX_OK;
+}
