@@ -208,6 +208,64 @@ int pmx_route_statistics(const int64_t* sel, const int64_t* src, int32_t src_con
                          int32_t E, int64_t T, int32_t K, int64_t* demand, int64_t* affinity,
                          int32_t* status, pmx_stream_t stream);
 
+/* ------------------------------------------------------------------------ */
+/* Expert-parallel payloads (the per-rank halves around the all-to-all)     */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of workspace pmx_ep_dispatch_payload needs. */
+size_t pmx_ep_payload_workspace_bytes(int64_t num_assign, int32_t num_ranks);
+
+/* Rank-deduplicated dispatch payload of one EP rank.  Assignment (t,k) with
+ * physical slot phys[t,k] goes to rank r = phys / slots_per_rank; a token's
+ * hidden row is sent once per distinct target rank.
+ *   assign_counts[r], assign_offsets[R+1]: assignments per target rank
+ *       (assignment_send_splits) and their exclusive prefix;
+ *   unique_counts[r], unique_offsets[R+1]: distinct (rank, token) pairs per
+ *       rank (unique_send_splits); U = unique_offsets[R];
+ *   send_hidden [U,H] bf16 (capacity T*K rows): row u = hidden[unique_tokens[u]],
+ *       pairs ordered by (rank, token);
+ *   unique_tokens [U] int32 (local_unique_token_indices);
+ *   send_meta [T*K,3] int32: (ordinal of the assignment's pair within its
+ *       rank, local slot, token) with assignments ordered by (rank, token, k);
+ *   send_weights [T*K] bf16: the routing weight of each, same order;
+ *   target_rank [T*K] int32 in (t,k) order.
+ * Ties within one (rank, token) pair keep k order (the reference sorts the
+ * keys with an unstable argsort, which leaves that order open).  phys: int32
+ * [T*K]; weights: bf16 [T*K]; hidden: bf16 [T,H], H % 8 == 0; K <= 32.  A
+ * slot outside [0, R*slots_per_rank) is clamped and sets *status (device
+ * int32, caller-zeroed) to 1.
+ * Replaces _build_local_payload
+ * (veomni/distributed/moe/hiermoe/all_to_all.py:979-1055). */
+int pmx_ep_dispatch_payload(const int32_t* phys, const void* hidden, const void* weights, int64_t T,
+                            int32_t K, int64_t H, int32_t R, int32_t slots_per_rank,
+                            int32_t* assign_counts, int32_t* assign_offsets, int32_t* unique_counts,
+                            int32_t* unique_offsets, void* send_hidden, int32_t* unique_tokens,
+                            int32_t* send_meta, void* send_weights, int32_t* target_rank,
+                            int32_t* status, void* workspace, size_t workspace_bytes,
+                            pmx_stream_t stream);
+
+/* Bytes of workspace pmx_ep_combine_aggregate needs for `num_recv` received
+ * assignments. */
+size_t pmx_ep_combine_workspace_bytes(int64_t num_recv);
+
+/* Combine on the rank that ran the experts: the weighted outputs of its N
+ * received assignments (receive order: source-rank major, tokens ascending
+ * within each source), summed in fp32 per run of equal (src_rank, src_token):
+ *   out[u] = bf16( sum_{a in run u} fp32( bf16(Y[pos[a]] * w[a]) ) ),
+ * where Y [*,H] bf16 holds the expert outputs in expert order and pos[a] is
+ * the row of assignment a in Y.  Outputs run_offsets [U+1] (capacity N+1),
+ * rank_runs [R] (runs per source rank: the combine send splits) and
+ * *num_runs = U, all on the device.  A source rank outside [0,R) sets
+ * *status (device int32, caller-zeroed) to 1.
+ * Replaces the unsort, weighting and _aggregate_weighted_outputs of
+ * rank_dedup_combine (veomni/distributed/moe/hiermoe/all_to_all.py:2553-2558,
+ * 2266-2294). */
+int pmx_ep_combine_aggregate(const void* Y, const int32_t* pos, const void* w, const int32_t* src_rank,
+                             const int32_t* src_token, int64_t N, int64_t H, int32_t R, void* out,
+                             int32_t* run_offsets, int32_t* rank_runs, int32_t* num_runs,
+                             int32_t* status, void* workspace, size_t workspace_bytes,
+                             pmx_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

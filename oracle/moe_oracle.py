@@ -33,6 +33,12 @@ How each function is pinned (the checks live in ``tests/test_oracle_*.py``):
 * ``replica_fold`` - the reference's known answer 10+2=12, 20+3=23
   (tests/distributed/test_hiermoe.py:3286-3338) and "sum of copy grads ==
   logical-expert grad of the eager model" (tests/distributed/test_hiermoe.py:3765-3778).
+* ``build_local_payload`` / ``aggregate_weighted_outputs`` - the reference's
+  known answer for the aggregation (tests/distributed/test_hiermoe.py:1116-1128),
+  a dictionary-based pure-Python payload on random inputs, and the
+  reference's own end-to-end check (test_hiermoe.py:1009-1011, the rank-dedup
+  dispatch + experts + combine equals the eager MoE at 1e-5, :935-996) with ranks simulated in
+  one process.
 * ``route_statistics`` - the reference's known answer (demand
   [[2,1,1,0],[0,1,1,2]] and the co-selection entries of
   tests/distributed/test_placemoe_optimizer.py:50-73), a pure-Python count
@@ -382,3 +388,66 @@ def route_statistics(samples, num_experts: int):
     for m in affinity:
         np.fill_diagonal(m, 0.0)
     return demand, affinity
+
+
+# ---------------------------------------------------------------------------
+# Expert-parallel payloads (per-rank halves around the all-to-all)
+# ---------------------------------------------------------------------------
+
+
+def build_local_payload(hidden: torch.Tensor, phys, weights: torch.Tensor, num_slots: int, ep_size: int) -> dict:
+    """``_build_local_payload`` (veomni/distributed/moe/hiermoe/all_to_all.py:979-1055):
+    assignments keyed by (target rank, token), sorted, deduplicated with
+    ``unique_consecutive``; one hidden row per key, one metadata row
+    (ordinal of the key within its rank, local slot, token) and weight per
+    assignment.  The reference sorts with an unstable argsort; here the sort
+    is stable (ties keep k order), one of the orders it may produce."""
+    phys = np.asarray(phys, dtype=np.int64)
+    T, K = phys.shape
+    L = num_slots // ep_size
+    flat = phys.reshape(-1)
+    ranks = flat // L
+    tokens = np.repeat(np.arange(T, dtype=np.int64), K)
+    stride = max(1, T)
+    keys = ranks * stride + tokens
+    order = np.argsort(keys, kind="stable")
+    skeys = keys[order]
+    change = np.ones(skeys.size, dtype=bool)
+    change[1:] = skeys[1:] != skeys[:-1]
+    inverse = np.cumsum(change) - 1
+    ukeys = skeys[change]
+    uranks = ukeys // stride
+    utokens = ukeys - uranks * stride
+    usplits = np.bincount(uranks, minlength=ep_size)
+    uoffsets = np.concatenate([[0], np.cumsum(usplits)[:-1]])
+    ordinal = (np.arange(ukeys.size) - uoffsets[uranks])[inverse]
+    meta = np.stack([ordinal, flat[order] - ranks[order] * L, tokens[order]], axis=1).astype(np.int32)
+    w = weights.reshape(-1)[torch.as_tensor(order)]
+    return {
+        "send_hidden": hidden[torch.as_tensor(utokens)],
+        "send_meta": meta,
+        "send_weights": w.reshape(-1, 1),
+        "unique_tokens": utokens,
+        "unique_send_splits": usplits.tolist(),
+        "assignment_send_splits": np.bincount(ranks, minlength=ep_size).tolist(),
+        "target_ranks": ranks.reshape(T, K),
+    }
+
+
+def aggregate_weighted_outputs(weighted: torch.Tensor, source_tokens, split_sizes, key_stride=None):
+    """``_aggregate_weighted_outputs`` (all_to_all.py:2266-2294): rows keyed by
+    (source rank, token) in receive order, ``unique_consecutive`` runs summed
+    with an fp32 ``index_add`` and cast back; returns (sums, runs per rank)."""
+    if weighted.numel() == 0:
+        return weighted[:0], []
+    src_ranks = np.repeat(np.arange(len(split_sizes)), split_sizes)
+    tokens = np.asarray(source_tokens, dtype=np.int64)
+    stride = max(1, int(key_stride) if key_stride is not None else tokens.size + 1)
+    keys = src_ranks * stride + tokens
+    change = np.ones(keys.size, dtype=bool)
+    change[1:] = keys[1:] != keys[:-1]
+    inverse = torch.as_tensor(np.cumsum(change) - 1)
+    ukeys = keys[change]
+    acc = torch.zeros((ukeys.size, weighted.shape[1]), dtype=torch.float32)
+    acc.index_add_(0, inverse, weighted.float())
+    return acc.to(weighted.dtype), np.bincount(ukeys // stride, minlength=len(split_sizes)).tolist()

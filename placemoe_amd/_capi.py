@@ -80,6 +80,18 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int32, c_void_p, c_void_p, c_void_p,
          c_void_p],
     ),
+    "pmx_ep_payload_workspace_bytes": (c_size_t, [c_int64, c_int32]),
+    "pmx_ep_dispatch_payload": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
+    "pmx_ep_combine_workspace_bytes": (c_size_t, [c_int64]),
+    "pmx_ep_combine_aggregate": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int32, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
 }
 
 _LIB = None

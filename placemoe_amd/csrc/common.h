@@ -75,6 +75,14 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 static inline int pmx_status(hipError_t e) { return e == hipSuccess ? PMX_OK : PMX_ERR_HIP; }
 
+// The routing path's stable counting sort (routing.hip), shared with the
+// expert-parallel payload builder (payload.hip); not part of the C ABI.
+__attribute__((visibility("hidden"))) int pmx_route_launch(
+    const int64_t* sel, const int64_t* M, const int64_t* src, int32_t src_const, int32_t S, int32_t E, int64_t A,
+    int32_t K, int32_t C, int32_t* phys, int32_t* counts, int32_t* offsets, int32_t* pos, void* workspace,
+    size_t workspace_bytes, hipStream_t stream);
+__attribute__((visibility("hidden"))) size_t pmx_route_ws_bytes(int64_t A, int32_t C);
+
 #define PMX_LAUNCH_CHECK()                         \
   do {                                             \
     hipError_t _e = hipGetLastError();             \

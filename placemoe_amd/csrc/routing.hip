@@ -489,6 +489,15 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 }  // namespace
 
+int pmx_route_launch(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t src_const, int32_t S,
+                     int32_t E, int64_t A, int32_t K, int32_t C, int32_t* phys, int32_t* counts, int32_t* offsets,
+                     int32_t* pos, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  return launch_route(sel, M, src, src_const, S, E, A, K, C, phys, counts, offsets, pos, workspace, workspace_bytes,
+                      stream);
+}
+
+size_t pmx_route_ws_bytes(int64_t A, int32_t C) { return route_ws_bytes(A, C); }
+
 extern "C" {
 
 const char* pmx_version(void) { return "placemoe_amd 0.1.0 gfx950"; }
