@@ -159,6 +159,79 @@ def cpu_baseline(wl, sample_tokens: int, backward: bool):
     return {"value": value, "unit": "ms", "cores": threads, "kind": "port", "sample": sample}
 
 
+def aux_measurements(wl, dev, reps: int = 10):
+    """Kernels beside the layer step, timed with HIP events around direct
+    C-ABI calls (preallocated buffers, no host synchronisation inside):
+    route-statistics capture, and the expert-parallel dispatch payload and
+    combine aggregation of this rank's routing split over 8 ranks."""
+    import ctypes
+
+    from placemoe_amd import _capi, kernels
+
+    lib = _capi.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    i32 = dict(dtype=torch.int32, device=dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps
+
+    T, K, H, C = wl.T, wl.K, wl.H, wl.C
+    A = T * K
+    ms, gbps = {}, {}
+    # route statistics: demand [S,E] and co-selection [S,E,E] counts
+    S = int(wl.mapping.shape[0]) if wl.sources is not None else 1
+    E = wl.num_experts
+    demand = torch.zeros((S, E), dtype=torch.int64, device=dev)
+    aff = torch.zeros((S, E, E), dtype=torch.int64, device=dev)
+    status = torch.zeros(1, **i32)
+    src = wl.sources.data_ptr() if wl.sources is not None else None
+    ms["route_statistics"] = timed(lambda: lib.pmx_route_statistics(
+        wl.selected.data_ptr(), src, 0, S, E, T, K, demand.data_ptr(), aff.data_ptr(), status.data_ptr(), stream))
+    # EP dispatch payload over R ranks of C/R slots
+    R = 8 if C % 8 == 0 else 4
+    r = kernels.route(wl.selected, C, mapping=wl.mapping, sources=wl.sources)
+    w = wl.routing_weights.contiguous()
+    outs = dict(ac=torch.empty(R, **i32), ao=torch.empty(R + 1, **i32), uc=torch.empty(R, **i32),
+                uo=torch.empty(R + 1, **i32), sh=torch.empty((A, H), dtype=torch.bfloat16, device=dev),
+                ut=torch.empty(A, **i32), meta=torch.empty((A, 3), **i32),
+                sw=torch.empty(A, dtype=torch.bfloat16, device=dev), tr=torch.empty(A, **i32))
+    ws = torch.empty(lib.pmx_ep_payload_workspace_bytes(A, R), dtype=torch.uint8, device=dev)
+    o = outs
+    ms["ep_dispatch_payload"] = timed(lambda: lib.pmx_ep_dispatch_payload(
+        r.phys.data_ptr(), wl.hidden.data_ptr(), w.data_ptr(), T, K, H, R, C // R, o["ac"].data_ptr(),
+        o["ao"].data_ptr(), o["uc"].data_ptr(), o["uo"].data_ptr(), o["sh"].data_ptr(), o["ut"].data_ptr(),
+        o["meta"].data_ptr(), o["sw"].data_ptr(), o["tr"].data_ptr(), status.data_ptr(), ws.data_ptr(),
+        ws.numel(), stream))
+    U = int(o["uc"].sum().item())
+    gbps["ep_dispatch_payload"] = (4 * U * H + 22 * A + 4 * U) / (ms["ep_dispatch_payload"] * 1e-3) / 1e9
+    # combine aggregation: this rank's assignments in send order as a receive buffer
+    src_rank = torch.repeat_interleave(torch.arange(R, device=dev, dtype=torch.int32), o["ac"].long())
+    src_tok = o["meta"][:, 2].contiguous()
+    y = torch.randn((A, H), device=dev).to(torch.bfloat16)
+    pos = r.pos.reshape(-1).contiguous()
+    out = torch.empty((A, H), dtype=torch.bfloat16, device=dev)
+    run_off = torch.empty(A + 1, **i32)
+    rank_runs = torch.empty(R, **i32)
+    nruns = torch.empty(1, **i32)
+    cws = torch.empty(lib.pmx_ep_combine_workspace_bytes(A), dtype=torch.uint8, device=dev)
+    ms["ep_combine_aggregate"] = timed(lambda: lib.pmx_ep_combine_aggregate(
+        y.data_ptr(), pos.data_ptr(), o["sw"].data_ptr(), src_rank.data_ptr(), src_tok.data_ptr(), A, H, R,
+        out.data_ptr(), run_off.data_ptr(), rank_runs.data_ptr(), nruns.data_ptr(), status.data_ptr(),
+        cws.data_ptr(), cws.numel(), stream))
+    Ur = int(nruns.item())
+    gbps["ep_combine_aggregate"] = (2 * A * H + 2 * Ur * H + 14 * A) / (ms["ep_combine_aggregate"] * 1e-3) / 1e9
+    return ({k: round(v, 4) for k, v in ms.items()}, {k: round(v, 1) for k, v in gbps.items()},
+            {"ep_ranks": R, "unique_rank_token_pairs": U})
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -282,6 +355,10 @@ def main():
                      "traffic": MEASURED_TRAFFIC_BYTES.get((args.config, dominant))},
         "cpu_baseline": None,
     }
+    aux_ms, aux_bw, aux_cfg = aux_measurements(wl, dev)
+    result["aux_kernel_ms"] = aux_ms
+    result["aux_bandwidth_gbps"] = aux_bw
+    result["aux_config"] = aux_cfg
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, args.cpu_sample_tokens, backward)
     print(json.dumps(result), flush=True)

@@ -165,7 +165,12 @@ __global__ __launch_bounds__(kScanBlock) void scan_blocks_kernel(int32_t* __rest
 }
 
 // Run starts -> run_offsets[run] = a (and run_offsets[U] = N); runs per
-// source rank.
+// source rank, counted in LDS per block (up to kLdsRanks ranks) and added to
+// the global counts once per block and rank: the ranks are sorted, so one
+// block touches few of them, and a global atomic per run would serialise on
+// R counters.
+constexpr int kLdsRanks = 4096;
+
 __global__ __launch_bounds__(kScanBlock) void run_offsets_kernel(const int32_t* __restrict__ flag,
                                                                  const int32_t* __restrict__ block_base,
                                                                  const int32_t* __restrict__ src_rank, int64_t N,
@@ -174,6 +179,10 @@ __global__ __launch_bounds__(kScanBlock) void run_offsets_kernel(const int32_t* 
                                                                  int32_t* __restrict__ rank_runs,
                                                                  int32_t* __restrict__ status) {
   __shared__ int32_t wsum[kScanBlock / 64];
+  __shared__ int32_t cnt[kLdsRanks];
+  const bool lds = R <= kLdsRanks;
+  if (lds)
+    for (int i = threadIdx.x; i < R; i += kScanBlock) cnt[i] = 0;
   const int64_t a = (int64_t)blockIdx.x * kScanBlock + threadIdx.x;
   const int32_t f = a < N ? flag[a] : 0;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -187,10 +196,19 @@ __global__ __launch_bounds__(kScanBlock) void run_offsets_kernel(const int32_t* 
     const int32_t run = before + __popcll(m & lt);
     run_offsets[run] = (int32_t)a;
     const int32_t r = src_rank[a];
-    if (r >= 0 && r < R) atomicAdd(&rank_runs[r], 1);
-    else atomicOr(status, 1);
+    if (r >= 0 && r < R) {
+      if (lds) atomicAdd(&cnt[r], 1);
+      else atomicAdd(&rank_runs[r], 1);
+    } else {
+      atomicOr(status, 1);
+    }
   }
   if (a == 0) run_offsets[*num_runs] = (int32_t)N;
+  if (lds) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < R; i += kScanBlock)
+      if (cnt[i]) atomicAdd(&rank_runs[i], cnt[i]);
+  }
 }
 
 // out[run] = bf16( sum_{a in run} fp32( bf16(Y[pos[a]] * w[a]) ) ); one block

@@ -3,15 +3,19 @@
 // accumulated on the device so that a profiling window needs no host copy of
 // the routes.
 //
-// One thread per token.  Counts are exact integers (64-bit device-scope
-// atomics into tables of S*E and S*E*E entries); the tables are small next to
-// the routing tensors and the updates of different tokens rarely collide.
+// One thread per token.  Counts are exact integers.  The demand table (S*E
+// entries) is counted per block in LDS when it fits and added to the global
+// table once per block and entry - with few experts every token would
+// otherwise hit the same few counters.  Co-selection pairs go straight to the
+// S*E*E table with 64-bit device-scope atomics; its entries are many and the
+// updates of different tokens rarely collide.
 
 #include "common.h"
 
 namespace {
 
 constexpr int kStatsMaxTopK = 32;
+constexpr int kLdsDemand = 8192;  // demand entries counted in LDS per block
 
 __global__ __launch_bounds__(256) void route_stats_kernel(const int64_t* __restrict__ sel,
                                                           const int64_t* __restrict__ src, int32_t src_const,
@@ -19,6 +23,12 @@ __global__ __launch_bounds__(256) void route_stats_kernel(const int64_t* __restr
                                                           unsigned long long* __restrict__ demand,
                                                           unsigned long long* __restrict__ affinity,
                                                           int32_t* __restrict__ status) {
+  __shared__ uint32_t lcount[kLdsDemand];
+  const int64_t SE = (int64_t)S * E;
+  const bool lds = SE <= kLdsDemand;
+  if (lds)
+    for (int64_t i = threadIdx.x; i < SE; i += blockDim.x) lcount[i] = 0u;
+  __syncthreads();
   for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < T; t += (int64_t)gridDim.x * blockDim.x) {
     const int64_t s = src != nullptr ? src[t] : (int64_t)src_const;
     const int64_t* row = sel + t * K;
@@ -30,7 +40,10 @@ __global__ __launch_bounds__(256) void route_stats_kernel(const int64_t* __restr
       continue;
     }
     const int64_t base = s * E;
-    for (int k = 0; k < K; ++k) atomicAdd(&demand[base + row[k]], 1ull);
+    for (int k = 0; k < K; ++k) {
+      if (lds) atomicAdd(&lcount[base + row[k]], 1u);
+      else atomicAdd(&demand[base + row[k]], 1ull);
+    }
     // Unordered pairs k < k' of distinct experts, counted in both orders; a
     // pair of equal experts would land on the diagonal, which stays zero.
     for (int a = 0; a < K; ++a) {
@@ -42,6 +55,11 @@ __global__ __launch_bounds__(256) void route_stats_kernel(const int64_t* __restr
         atomicAdd(&affinity[(base + eb) * E + ea], 1ull);
       }
     }
+  }
+  if (lds) {
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < SE; i += blockDim.x)
+      if (lcount[i]) atomicAdd(&demand[i], (unsigned long long)lcount[i]);
   }
 }
 
