@@ -39,10 +39,10 @@ PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 # what the counter reads for a 1 GiB device copy: x2.00 and x1.00).  Counters
 # cannot be read from inside a timed run, so the figure is carried here.
 MEASURED_TRAFFIC_BYTES = {
-    ("qwen3", "fc1_fwd"): (2407 + 576) * 2**20,
-    ("qwen3", "fc1_wgrad"): (1858 + 960) * 2**20,
-    ("dsv3", "fc1_fwd"): (6326 + 769) * 2**20,
-    ("dsv3", "fc1_dgrad"): (6366 + 896) * 2**20,
+    ("qwen3", "fc1_fwd"): (2454 + 576) * 2**20,
+    ("qwen3", "fc1_wgrad"): (2011 + 960) * 2**20,
+    ("dsv3", "fc1_fwd"): (6547 + 768) * 2**20,
+    ("dsv3", "fc1_dgrad"): (6534 + 896) * 2**20,
 }
 
 # Entry-point call order inside one step; repeated names are told apart by
@@ -105,6 +105,8 @@ def parse():
     p.add_argument("--profile-steps", type=int, default=5, help="extra steps timed per kernel with HIP events")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first run a plain 1 GiB device copy (reference kernel for HBM-traffic counters)")
+    p.add_argument("--vendor-gemm", action="store_true",
+                   help="also time the six GEMMs through hipBLASLt, one call per copy, on the same groups")
     return p.parse_args()
 
 
@@ -230,6 +232,61 @@ def aux_measurements(wl, dev, reps: int = 10):
     gbps["ep_combine_aggregate"] = (2 * A * H + 2 * Ur * H + 14 * A) / (ms["ep_combine_aggregate"] * 1e-3) / 1e9
     return ({k: round(v, 4) for k, v in ms.items()}, {k: round(v, 1) for k, v in gbps.items()},
             {"ep_ranks": R, "unique_rank_token_pairs": U})
+
+
+def vendor_gemms(wl, dev, reps: int = 5):
+    """The layer's six GEMMs on the same per-copy row groups through the
+    vendor library (hipBLASLt via torch.matmul, one call per non-empty copy),
+    timed with HIP events: a library reference for the grouped kernel."""
+    from placemoe_amd import kernels
+
+    H, I = wl.H, wl.I
+    r = kernels.route(wl.selected, wl.C, mapping=wl.mapping, sources=wl.sources)
+    counts = [int(c) for c in r.counts.cpu().tolist()]
+    g = torch.Generator(device=dev).manual_seed(5)
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    A = sum(counts)
+    x = torch.randn((A, H), generator=g, device=dev).to(torch.bfloat16)
+    act = torch.randn((A, I), generator=g, device=dev).to(torch.bfloat16)
+    dy = torch.randn((A, H), generator=g, device=dev).to(torch.bfloat16)
+    dg1 = torch.randn((A, 2 * I), generator=g, device=dev).to(torch.bfloat16)
+    w1, w2 = wl.fc1.detach(), wl.fc2.detach()
+    rows, o = [], 0
+    for c, n in enumerate(counts):
+        if n:
+            rows.append((c, slice(o, o + n)))
+        o += n
+    outs = {"fc1_fwd": torch.empty((A, 2 * I), **bf), "fc2_fwd": torch.empty((A, H), **bf),
+            "fc2_dgrad": torch.empty((A, I), **bf), "fc1_dgrad": torch.empty((A, H), **bf),
+            "fc2_wgrad": torch.empty((wl.C, H, I), **bf), "fc1_wgrad": torch.empty((wl.C, 2 * I, H), **bf)}
+    calls = {
+        "fc1_fwd": lambda c, s: torch.matmul(x[s], w1[c].t(), out=outs["fc1_fwd"][s]),
+        "fc2_fwd": lambda c, s: torch.matmul(act[s], w2[c].t(), out=outs["fc2_fwd"][s]),
+        "fc2_dgrad": lambda c, s: torch.matmul(dy[s], w2[c], out=outs["fc2_dgrad"][s]),
+        "fc2_wgrad": lambda c, s: torch.matmul(dy[s].t(), act[s], out=outs["fc2_wgrad"][c]),
+        "fc1_wgrad": lambda c, s: torch.matmul(dg1[s].t(), x[s], out=outs["fc1_wgrad"][c]),
+        "fc1_dgrad": lambda c, s: torch.matmul(dg1[s], w1[c], out=outs["fc1_dgrad"][s]),
+    }
+    flops = {"fc1_fwd": 2 * A * H * 2 * I, "fc2_fwd": 2 * A * I * H, "fc2_dgrad": 2 * A * H * I,
+             "fc2_wgrad": 2 * A * H * I, "fc1_wgrad": 2 * A * 2 * I * H, "fc1_dgrad": 2 * A * 2 * I * H}
+    ms = {}
+    for name, fn in calls.items():
+        for c, s in rows:
+            fn(c, s)
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(reps):
+            for c, s in rows:
+                fn(c, s)
+        s1.record()
+        torch.cuda.synchronize()
+        ms[name] = s0.elapsed_time(s1) / reps
+    total = sum(ms.values())
+    return {"library": "hipBLASLt (torch.matmul), one call per non-empty copy",
+            "kernel_ms": {k: round(v, 4) for k, v in ms.items()},
+            "tflops": {k: round(flops[k] / (ms[k] * 1e-3) / 1e12, 1) for k in ms},
+            "gemm_tflops": round(sum(flops.values()) / (total * 1e-3) / 1e12, 1)}
 
 
 def main():
@@ -359,6 +416,8 @@ def main():
     result["aux_kernel_ms"] = aux_ms
     result["aux_bandwidth_gbps"] = aux_bw
     result["aux_config"] = aux_cfg
+    if args.vendor_gemm:
+        result["vendor_gemm"] = vendor_gemms(wl, dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, args.cpu_sample_tokens, backward)
     print(json.dumps(result), flush=True)

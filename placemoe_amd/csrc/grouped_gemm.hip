@@ -53,7 +53,6 @@ constexpr int NWAVES = 8, WAVES_N = 4;
 constexpr int NTHREADS = 64 * NWAVES;
 constexpr int WROWS = 128, WCOLS = 64;  // output tile of one wave
 constexpr int MT = WROWS / 32, NTT = WCOLS / 32;
-constexpr int EPI_BYTES = 16 * WCOLS * 2;  // per wave: 16 output rows
 constexpr int kMaxGroups = 2048;
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always fails the range check
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
@@ -330,7 +329,7 @@ __device__ __forceinline__ void mma_some(const Frags<BM>& f, f32x16_t (&acc)[MT]
 #pragma unroll
   for (int x = I; x < I + N; ++x)
     acc[x / NTT][x % NTT] =
-        __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[x / NTT], f.b[x % NTT], acc[x / NTT][x % NTT], 0, 0, 0);
+        __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[x % NTT], f.a[x / NTT], acc[x / NTT][x % NTT], 0, 0, 0);
 }
 
 template <int BM>
@@ -339,7 +338,7 @@ __device__ __forceinline__ void mma_frags(const Frags<BM>& f, f32x16_t (&acc)[MT
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NTT; ++nt)
-      acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[mt], f.b[nt], acc[mt][nt], 0, 0, 0);
+      acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[nt], f.a[mt], acc[mt][nt], 0, 0, 0);
 }
 
 // Compile-time loop: f(Int<I>{}) for I = B .. E-1, so that accumulator
@@ -366,87 +365,98 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[MT][NTT]) {
       for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
 }
 
-// Output element i of acc[mt][nt] in lane l sits at row
-// (i/4)*8 + (l/32)*4 + i%4, column l%32 of the 32x32 tile.
+// The MFMAs take the B fragment as their first operand, so each accumulator
+// holds its 32 x 32 output tile transposed: element i of acc[mt][nt] in lane
+// l is output row l%32, column 8*(i/4) + 4*(l/32) + i%4.  A lane therefore
+// holds runs of 4 consecutive columns of one row, which go to LDS as single
+// 8-byte writes.
 //
-// Epilogue: each wave stages its 128 x 64 output tile in rounds of 16 rows as
-// bf16 in its own 2 KB of LDS (row-major, 128-byte rows, 16-byte chunks
-// XOR-swizzled by bit 2 of the row so the two half-waves' 2-byte stores use
-// different banks), then reads each round back one 16-byte chunk per lane
-// and writes whole row segments.  A wave's LDS operations complete in order,
-// so a round may overwrite what the previous one read.
+// Epilogue: the wave's 128 x 64 output tile passes through LDS as bf16 in two
+// rounds of 64 rows (8 KB), then leaves as 16-byte row segments, eight rows of
+// 128 bytes per store instruction.  The staging area is the wave's own share
+// of the stage just freed: the eight 1 KB chunks k*NWAVES + wave that its
+// buffer->LDS loads fill, so no other wave reads or writes them until this
+// wave issues its next loads.  Rows of a round are 128 bytes; 16-byte chunk c
+// of row r sits at c ^ ((r >> 1) & 7).
 
-__device__ __forceinline__ int epi_swz(int row) { return ((row >> 2) & 1) << 2; }
-
-__device__ __forceinline__ int epi_off(int row, int col) {
-  return row * (WCOLS * 2) + (((col >> 3) ^ epi_swz(row)) << 4) + (col & 7) * 2;
+__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
+  return make_uint2(f32_to_bf16(a) | (f32_to_bf16(b) << 16), f32_to_bf16(c) | (f32_to_bf16(d) << 16));
 }
 
-// Round r: rows 16r .. 16r+15 of the wave's tile, i.e. acc[r/2][.][8*(r%2) .. +7].
-template <typename F>
-__device__ __forceinline__ void stage_round(char* region, int lane, int r, int ncols, F value) {
-  const int cl = lane & 31;
-  const int rq = (lane >> 5) * 4;
-  const int mt = r >> 1, i0 = (r & 1) * 8;
+// Byte offset, inside the stage, of byte `x` of row r (0..63) of the wave's staging area.
+__device__ __forceinline__ int epi_off(int wave, int r, int x) {
+  const int chunk = (x >> 4) ^ ((r >> 1) & 7);
+  return ((r >> 3) * NWAVES + wave) * 1024 + (r & 7) * 128 + (chunk << 4) + (x & 15);
+}
+
+// Stage rows 64*half .. +63 of the wave's tile from `v(mt, nt, i)` (columns
+// 0 .. 32*NC-1 of the wave's 64), as bf16.
+template <int NC, typename F>
+__device__ __forceinline__ void stage_half(char* stage, int wave, int lane, int half, F v) {
+  const int rl = lane & 31, h = lane >> 5;
 #pragma unroll
-  for (int nt = 0; nt < NTT; ++nt)
+  for (int mtl = 0; mtl < 2; ++mtl)
 #pragma unroll
-    for (int ii = 0; ii < 8; ++ii) {
-      if (nt * 32 < ncols) {
-        const int row = (ii >> 2) * 8 + rq + (ii & 3);
-        *reinterpret_cast<bf16_t*>(region + epi_off(row, nt * 32 + cl)) = (bf16_t)f32_to_bf16(value(mt, nt, i0 + ii));
+    for (int nt = 0; nt < NC; ++nt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int mt = 2 * half + mtl;
+        const int r = mtl * 32 + rl;
+        const int col = nt * 32 + 8 * j + 4 * h;
+        *reinterpret_cast<uint2*>(stage + epi_off(wave, r, col * 2)) =
+            pack4(v(mt, nt, 4 * j), v(mt, nt, 4 * j + 1), v(mt, nt, 4 * j + 2), v(mt, nt, 4 * j + 3));
       }
-    }
 }
 
-__device__ __forceinline__ uint4 staged_chunk(const char* region, int row, int chunk) {
-  return *reinterpret_cast<const uint4*>(region + row * (WCOLS * 2) + ((chunk ^ epi_swz(row)) << 4));
+__device__ __forceinline__ uint4 staged_chunk(const char* stage, int wave, int r, int chunk) {
+  return *reinterpret_cast<const uint4*>(stage + epi_off(wave, r, chunk * 16));
 }
 
 template <int KIND, int BM>
-__device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti, int wm, int wn, int lane,
-                                         const f32x16_t (&acc)[MT][NTT], char* region) {
+__device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti, int wm, int wn, int wave, int lane,
+                                         const f32x16_t (&acc)[MT][NTT], char* stage) {
   // The lane index passes through an opaque move so that the epilogue's
   // per-lane address arithmetic stays here instead of being hoisted out of
   // the tile loop, where it would hold registers through every K step.
   asm volatile("" : "+v"(lane));
-  const int cc = lane & 7;  // read-back chunk (8 columns) of the 64-column tile
-  static_for<0, WROWS / 16>([&](auto round) {
-    constexpr int r = decltype(round)::value;
-    const int64_t rb = wm * WROWS + r * 16;  // first row of the round within the tile
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int64_t rb = wm * WROWS + half * 64;  // first tile row of the round
     if constexpr (KIND == KIND_FC1) {
       // The wave's 64 columns are 32 gate and the matching 32 up columns:
       // first both as bf16 GEMM outputs (gu), then act = bf16(bf16(silu(gate)) * up).
       const int64_t I = P.I;
       const int64_t j0 = (int64_t)ti.ntile * 128 + wn * 32;
-      stage_round(region, lane, r, 64, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      stage_half<2>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      const int cc = lane & 7;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int rl = (lane >> 3) + 8 * q;
+      for (int q = 0; q < 8; ++q) {
+        const int rl = q * 8 + (lane >> 3);
         const int64_t row = ti.row0 + rb + rl;
-        const uint4 v = staged_chunk(region, rl, cc);
+        const uint4 v = staged_chunk(stage, wave, rl, cc);
         const int64_t j = j0 + (cc & 3) * 8;
         if (row < ti.row_end && j < I) *reinterpret_cast<uint4*>(P.gu + row * 2 * I + (cc < 4 ? 0 : I) + j) = v;
       }
-      stage_round(region, lane, r, 32, [&](int mt, int nt, int i) {
-        const float gb = round_bf16(acc[mt][0][i]);
-        const float ub = round_bf16(acc[mt][1][i]);
-        return round_bf16(silu_f32(gb)) * ub;
+      stage_half<1>(stage, wave, lane, half, [&](int mt, int, int i) {
+        return round_bf16(silu_f32(round_bf16(acc[mt][0][i]))) * round_bf16(acc[mt][1][i]);
       });
-      {
-        const int rl = lane >> 2, c4 = lane & 3;
+      const int c4 = lane & 3;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int rl = q * 16 + (lane >> 2);
         const int64_t row = ti.row0 + rb + rl;
-        const uint4 v = staged_chunk(region, rl, c4);
+        const uint4 v = staged_chunk(stage, wave, rl, c4);
         const int64_t j = j0 + c4 * 8;
         if (row < ti.row_end && j < I) *reinterpret_cast<uint4*>(P.act + row * I + j) = v;
       }
     } else {
-      stage_round(region, lane, r, 64, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      const int cc = lane & 7;  // 16-byte chunk (8 columns) of the wave's 64
       const int64_t col = (int64_t)ti.ntile * BN + wn * WCOLS + cc * 8;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int rl = (lane >> 3) + 8 * q;
-        const uint4 v = staged_chunk(region, rl, cc);
+      for (int q = 0; q < 8; ++q) {
+        const int rl = q * 8 + (lane >> 3);
+        const uint4 v = staged_chunk(stage, wave, rl, cc);
         if constexpr (KIND == KIND_TN) {
           const int64_t m = (int64_t)ti.mtile * BM + rb + rl;
           if (m < P.M && col < P.N) {
@@ -461,7 +471,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
     }
     // Keep each round's loads and stores in their round (register pressure).
     asm volatile("" ::: "memory");
-  });
+  }
 }
 
 // The partial last K-tile of a K of `K` (-1 if none) and its valid k.
@@ -659,6 +669,9 @@ __device__ __forceinline__ void wait_loads_lds() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(PENDING) : "memory");
 }
 
+// Wait until this wave's LDS reads and writes have completed.
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // Workgroup barrier that neither the compiler's memory model nor its
 // scheduler moves anything across: memory operations stay on their side (the
 // asm clobbers memory), and so do the MFMAs, so that every LDS read consumed
@@ -694,7 +707,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
   constexpr int QA = loads_per_wave<BM>(), QB = loads_per_wave<BN>();  // per wave and K-tile
   __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char epi[NWAVES * EPI_BYTES];
   __shared__ int32_t tpre[kMaxGroups + 1];
   __shared__ int32_t scan_buf[NTHREADS];
   const int t = threadIdx.x;
@@ -873,15 +885,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       }
       zero_tile<BM>(P, cur, t);
     }
-    // The stage of the tile's last K-tile is free (barrier above): the next
-    // stream K-tile goes there while this tile is finished and written out.
-    issue_next(lds + (cs ^ 1) * STAGE_BYTES);
+    // The stage of the tile's last K-tile is free (barrier above): each wave
+    // stages its output in its own chunks of it, then, once its LDS reads
+    // have returned, issues the next stream K-tile into the same chunks.
     mma_frags<BM>(f1, acc);
-    epilogue<KIND, BM>(P, done, wm, wn, lane, acc, epi + wave * EPI_BYTES);
+    epilogue<KIND, BM>(P, done, wm, wn, wave, lane, acc, lds + (cs ^ 1) * STAGE_BYTES);
     if (!more) {
       wait_loads<0>();
       return;
     }
+    wait_lds();
+    issue_next(lds + (cs ^ 1) * STAGE_BYTES);
   }
 }
 
