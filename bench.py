@@ -230,8 +230,68 @@ def aux_measurements(wl, dev, reps: int = 10):
         cws.data_ptr(), cws.numel(), stream))
     Ur = int(nruns.item())
     gbps["ep_combine_aggregate"] = (2 * A * H + 2 * Ur * H + 14 * A) / (ms["ep_combine_aggregate"] * 1e-3) / 1e9
-    return ({k: round(v, 4) for k, v in ms.items()}, {k: round(v, 1) for k, v in gbps.items()},
-            {"ep_ranks": R, "unique_rank_token_pairs": U})
+    cfg = {"ep_ranks": R, "unique_rank_token_pairs": U}
+    del outs, o, ws, y, out, cws
+    cfg.update(replica_exchange_measurement(wl, dev, R, ms, gbps))
+    return ({k: round(v, 4) for k, v in ms.items()}, {k: round(v, 1) for k, v in gbps.items()}, cfg)
+
+
+def replica_exchange_measurement(wl, dev, R, ms, gbps):
+    """Rank 0's side of the cross-rank replica-gradient exchange with the
+    workload's copies split over R ranks (C/R slots each): its pack and its
+    finish (the received buffers are the other ranks' real packs), bf16 copy
+    gradients of the layer's shapes."""
+    from placemoe_amd.replica import ReplicaGradExchange, replica_grad_schedule
+
+    C, H, I = wl.C, wl.H, wl.I
+    nl = C // R
+    L = np.asarray(wl.slot_to_logical)
+    owners = np.asarray(wl.owner_slots())
+    sched = [replica_grad_schedule(L, owners, nl, r, R) for r in range(R)]
+    g = torch.Generator(device=dev).manual_seed(11)
+    grads = [(torch.randn((nl, 2 * I, H), generator=g, device=dev).to(torch.bfloat16),
+              torch.randn((nl, H, I), generator=g, device=dev).to(torch.bfloat16)) for _ in range(R)]
+    ex = [ReplicaGradExchange(sched[r], r, grads[r]) for r in range(R)]
+    pairwise = sched[0].pairwise
+    sends = [e.pairwise_send() if pairwise else e.owner_reduce_send() for e in ex]
+    recv0 = {}
+    for src, per_dtype in enumerate(sends):
+        for dtype, bufs in per_dtype.items():
+            if 0 in bufs:
+                recv0.setdefault(dtype, {})[src] = bufs[0]
+    pack = ex[0].pairwise_send if pairwise else ex[0].owner_reduce_send
+    finish = ex[0].pairwise_finish if pairwise else ex[0].owner_reduce_finish
+
+    def kernel_ms(fn, entry, reps=5):
+        # HIP events around each launch only: the host builds the item tables
+        # between launches, which is not kernel time.
+        from placemoe_amd import _capi
+
+        fn()
+        timer = EventTimer()
+        _capi.set_timer(timer)
+        for _ in range(reps):
+            timer.new_step()
+            fn()
+        _capi.set_timer(None)
+        return sum(v for (name, _), v in timer.averages().items() if name == entry)
+
+    b = ex[0].bytes_moved
+    pack()
+    per_pack = ex[0].bytes_moved - b
+    ms["replica_exchange_pack"] = kernel_ms(pack, "pmx_replica_exchange_pack")
+    b = ex[0].bytes_moved
+    finish(recv0)
+    per_finish = ex[0].bytes_moved - b
+    ms["replica_exchange_finish"] = kernel_ms(lambda: finish(recv0), "pmx_replica_exchange_unpack")
+    if per_pack:
+        gbps["replica_exchange_pack"] = per_pack / (ms["replica_exchange_pack"] * 1e-3) / 1e9
+    if per_finish:
+        gbps["replica_exchange_finish"] = per_finish / (ms["replica_exchange_finish"] * 1e-3) / 1e9
+    return {"replica_exchange": {"ranks": R, "slots_per_rank": nl, "pairwise": pairwise,
+                                 "groups_on_rank0": sum(1 for x in sched[0].groups if x.local_slots),
+                                 "remote_peers_rank0": sorted(next(iter(recv0.values()), {}).keys()),
+                                 "pack_bytes": per_pack, "finish_bytes": per_finish}}
 
 
 def vendor_gemms(wl, dev, reps: int = 5):

@@ -190,6 +190,42 @@ int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const int32_t* co
                      int32_t writeback, pmx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Cross-rank replica-gradient exchange: the per-rank halves                 */
+/* ------------------------------------------------------------------------ */
+
+/* Gradient element types of the exchange entry points. */
+#define PMX_DTYPE_BF16 0
+#define PMX_DTYPE_F32 1
+
+/* An exchange item is one logical expert x one parameter.  grads: [C, P]
+ * copy gradients of this rank (`dtype`), item i's local copies are
+ * slots[slot_offsets[i] .. slot_offsets[i+1]).  Pointer lists hold device
+ * addresses (int64) of P-element regions: item i's outputs are
+ * out_ptrs[out_offsets[i] .. out_offsets[i+1]), its received parts
+ * part_ptrs[part_offsets[i] .. part_offsets[i+1]).  Sums accumulate in fp32
+ * (local slots in list order, then parts in list order) and are stored once
+ * in `dtype`.  A slot outside [0, C) is skipped and sets *status to 1.
+ *
+ * pack:   out = sum of the item's local copies, written to each output
+ *         region (the send buffers).  Replaces the local sums of
+ *         _replica_grad_contributions (expert_swap.py:6839-6876) and
+ *         _pack_replica_grad_items (:6907-6929).
+ * unpack: total = (with_local ? sum of local copies : 0) + sum of parts,
+ *         written into every local copy and to each output region (an
+ *         owner's broadcast buffers; out lists may be NULL).  Replaces the
+ *         receive halves of _sync_pairwise_replica_gradients (:7038-7107:
+ *         local_sum + remote), _sync_owner_replica_gradients (:7109-7217:
+ *         owner total and broadcast) and _unpack_replica_grad (:6886-6889).
+ * The transfer between ranks (RCCL send/recv or all-to-all) is the caller's. */
+int pmx_replica_exchange_pack(const void* grads, int32_t dtype, int64_t P, int32_t C, int32_t n_items,
+                              const int32_t* slot_offsets, const int32_t* slots, const int32_t* out_offsets,
+                              const int64_t* out_ptrs, int32_t* status, pmx_stream_t stream);
+int pmx_replica_exchange_unpack(void* grads, int32_t dtype, int64_t P, int32_t C, int32_t n_items,
+                                const int32_t* slot_offsets, const int32_t* slots, int32_t with_local,
+                                const int32_t* part_offsets, const int64_t* part_ptrs, const int32_t* out_offsets,
+                                const int64_t* out_ptrs, int32_t* status, pmx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Route statistics for the placement planner                               */
 /* ------------------------------------------------------------------------ */
 

@@ -451,3 +451,94 @@ def aggregate_weighted_outputs(weighted: torch.Tensor, source_tokens, split_size
     acc = torch.zeros((ukeys.size, weighted.shape[1]), dtype=torch.float32)
     acc.index_add_(0, inverse, weighted.float())
     return acc.to(weighted.dtype), np.bincount(ukeys // stride, minlength=len(split_sizes)).tolist()
+
+
+# ---------------------------------------------------------------------------
+# Cross-rank replica-gradient exchange (all ranks simulated in one process)
+# ---------------------------------------------------------------------------
+
+
+def replica_grad_schedule(slot_to_logical, logical_to_physical, num_local: int, ep_rank: int, ep_size: int):
+    """``_replica_grad_schedule_for_layer`` (expert_swap.py:6797-6837) over
+    ``redundant_copy_groups`` (:552-572), owners from
+    ``_owner_rank_for_copy_group`` (:6541-6555).  Returns a dict with
+    ``groups`` = [(logical, owner_rank, copy_ranks, local_slots)], ``pairwise``
+    and ``globally_ordered_pairs``."""
+    L = np.asarray(slot_to_logical, dtype=np.int64)
+    owners = np.asarray(logical_to_physical, dtype=np.int64)
+    active = L[L >= 0]
+    counts = np.bincount(active, minlength=owners.size) if active.size else np.zeros(owners.size, np.int64)
+    groups = []
+    for e in np.nonzero(counts > 1)[0]:
+        slots = [int(s) for s in np.nonzero(L == e)[0]]
+        owner_slot = int(owners[e])
+        if owner_slot not in slots:
+            raise RuntimeError(f"HierMoE owner slot {owner_slot} for logical expert {int(e)} is not in its copy group.")
+        copy_ranks = tuple(sorted({s // num_local for s in slots}))
+        local = tuple(s % num_local for s in slots if s // num_local == ep_rank)
+        groups.append((int(e), owner_slot // num_local, copy_ranks, local))
+    pairwise = all(len(g[2]) <= 2 for g in groups)
+    neighbors = [set() for _ in range(ep_size)]
+    if pairwise:
+        for _, _, ranks, _ in groups:
+            if len(ranks) == 2:
+                a, b = ranks
+                neighbors[a].add(b)
+                neighbors[b].add(a)
+    ordered = pairwise and any(len(n) > 1 for n in neighbors)
+    return {"groups": groups, "pairwise": pairwise, "globally_ordered_pairs": ordered}
+
+
+def replica_grad_sync(rank_grads, slot_to_logical, logical_to_physical, num_local: int):
+    """``sync_redundant_gradients`` (expert_swap.py:7220-7252) of every rank at
+    once.  ``rank_grads[r]`` is the tuple of rank r's copy gradients (one
+    tensor [num_local, ...] per parameter, gate_up then down); returns new
+    tuples.  Arithmetic follows the reference in the gradient dtype: local
+    sums by ``clone`` + ``add_`` in slot order (:6839-6876); pairwise totals
+    ``local_sum + remote`` (:7038-7107); owner totals ``local_sum`` plus each
+    source's part in the order the owner's receive list first meets the
+    source ranks (:7109-7217); every local copy then takes the total
+    (``_unpack_replica_grad``, :6886-6889)."""
+    R = len(rank_grads)
+    out = [tuple(g.clone() for g in grads) for grads in rank_grads]
+    scheds = [replica_grad_schedule(slot_to_logical, logical_to_physical, num_local, r, R) for r in range(R)]
+    pairwise = scheds[0]["pairwise"]
+    # The owner's receive dict meets source ranks group by group, in rank order.
+    peer_order = {r: [] for r in range(R)}
+    for _, owner, ranks, _ in scheds[0]["groups"]:
+        for q in ranks:
+            if q != owner and q not in peer_order[owner]:
+                peer_order[owner].append(q)
+
+    def local_sum(r, slots, p):
+        s = rank_grads[r][p][slots[0]].clone()
+        for c in slots[1:]:
+            s.add_(rank_grads[r][p][c])
+        return s
+
+    for gi, (e, owner, ranks, _) in enumerate(scheds[0]["groups"]):
+        local = {r: scheds[r]["groups"][gi][3] for r in ranks}
+        for p in range(len(rank_grads[0])):
+            sums = {r: local_sum(r, local[r], p) for r in ranks}
+            if pairwise:
+                totals = {r: sums[r] + sums[q] for r in ranks for q in ranks if q != r} if len(ranks) == 2 \
+                    else {r: sums[r] for r in ranks}
+            else:
+                total = sums[owner].clone()
+                for src in sorted((q for q in ranks if q != owner), key=peer_order[owner].index):
+                    total.add_(sums[src])
+                totals = {r: total for r in ranks}
+            for r in ranks:
+                for c in local[r]:
+                    out[r][p][c].copy_(totals[r])
+    return out
+
+
+def owner_grad_norm_mask(logical_to_physical, num_local: int, ep_rank: int):
+    """``redundant_grad_norm_masks`` (expert_swap.py:7254-7266): True at the
+    local slots of this rank that are the runtime owner of their expert."""
+    mask = np.zeros(num_local, dtype=bool)
+    for s in np.asarray(logical_to_physical, dtype=np.int64):
+        if s // num_local == ep_rank:
+            mask[s % num_local] = True
+    return mask

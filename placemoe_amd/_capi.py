@@ -75,6 +75,16 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, POINTER(c_float), c_int32,
          c_void_p],
     ),
+    "pmx_replica_exchange_pack": (
+        c_int,
+        [c_void_p, c_int32, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p],
+    ),
+    "pmx_replica_exchange_unpack": (
+        c_int,
+        [c_void_p, c_int32, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
     "pmx_route_statistics": (
         c_int,
         [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int32, c_void_p, c_void_p, c_void_p,
