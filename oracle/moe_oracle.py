@@ -44,6 +44,12 @@ How each function is pinned (the checks live in ``tests/test_oracle_*.py``):
   tests/distributed/test_placemoe_optimizer.py:50-73), a pure-Python count
   over token pairs on random samples, and the invariants sum(demand[s]) =
   T_s*K, symmetry, zero diagonal, sum(affinity[s]) = 2 * #distinct pairs.
+* ``replica_grad_schedule`` / ``replica_grad_sync`` / ``owner_grad_norm_mask``
+  - the reference's three known answers (the 2-rank cover 12 / 23,
+  tests/distributed/test_hiermoe.py:3200-3338; the three-copy owner exchange
+  6 / 60, :3545-3592; the 4-rank pair graph, :3480-3540) with their
+  pairwise / globally-ordered flags, and on random layouts the invariant that
+  every copy ends with the exact sum of its expert's copies.
 """
 
 from __future__ import annotations
