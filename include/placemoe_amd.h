@@ -12,6 +12,9 @@
  *    synchronises the host, and enqueues work only on the given stream.
  *  - bf16 tensors are passed as `const void*` holding bf16 bit patterns,
  *    row-major and contiguous.  Index tensors are int32 unless stated.
+ *  - Positions, row offsets and the row kernels' token rows are 32-bit:
+ *    assignments T*K, GEMM row counts and segment-sum rows above 2^31-1
+ *    return PMX_ERR_SHAPE before anything is launched.
  *  - Each declaration names the reference (pia7a/PlaceMoE) interface it
  *    replaces, as `file:line`.
  */

@@ -978,7 +978,7 @@ int pmx_gemm_fc1_swiglu_fwd(const void* X, const void* w_gate, const void* w_up,
                             const int32_t* offsets, int32_t G, int64_t A, int64_t H, int64_t I, void* gu,
                             void* act, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || A < 0 || H <= 0 || I <= 0) return PMX_ERR_ARG;
-  if (H % 8 || I % 8) return PMX_ERR_SHAPE;
+  if (H % 8 || I % 8 || A > INT32_MAX) return PMX_ERR_SHAPE;  // row offsets are int32
   if (A == 0) return PMX_OK;
   if (!X || !w_gate || !w_up || !offsets || !gu || !act) return PMX_ERR_ARG;
   if (!a16(X) || !a16(w_gate) || !a16(w_up)) return PMX_ERR_SHAPE;
@@ -1003,7 +1003,7 @@ int pmx_gemm_fc1_swiglu_fwd(const void* X, const void* w_gate, const void* w_up,
 int pmx_group_gemm_nt(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
                       int64_t K, void* C, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || M < 0 || N <= 0 || K <= 0) return PMX_ERR_ARG;
-  if (N % 8 || K % 8) return PMX_ERR_SHAPE;
+  if (N % 8 || K % 8 || M > INT32_MAX) return PMX_ERR_SHAPE;  // row offsets are int32
   if (M == 0) return PMX_OK;
   if (!A || !B || !offsets || !C) return PMX_ERR_ARG;
   if (!a16(A) || !a16(B)) return PMX_ERR_SHAPE;
@@ -1024,7 +1024,7 @@ int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_c
                       const int32_t* offsets, int32_t G, int64_t M, int64_t N, int64_t K, void* C,
                       pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || M < 0 || N <= 0 || K <= 0) return PMX_ERR_ARG;
-  if (N % 8 || K % 8) return PMX_ERR_SHAPE;
+  if (N % 8 || K % 8 || M > INT32_MAX) return PMX_ERR_SHAPE;  // row offsets are int32
   if (M == 0) return PMX_OK;
   if (!A || !B0 || !offsets || !C) return PMX_ERR_ARG;
   if (!a16(A) || !a16(B0) || (B1 && !a16(B1))) return PMX_ERR_SHAPE;
@@ -1050,7 +1050,7 @@ int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_c
 int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void* gu, const int32_t* offsets,
                                   int32_t G, int64_t A, int64_t H, int64_t I, void* dG1, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || A < 0 || H <= 0 || I <= 0) return PMX_ERR_ARG;
-  if (H % 8 || I % 8) return PMX_ERR_SHAPE;
+  if (H % 8 || I % 8 || A > INT32_MAX) return PMX_ERR_SHAPE;  // row offsets are int32
   if (A == 0) return PMX_OK;
   if (!dY || !w_down || !gu || !offsets || !dG1) return PMX_ERR_ARG;
   if (!a16(dY) || !a16(w_down) || !a16(gu) || !a16(dG1)) return PMX_ERR_SHAPE;

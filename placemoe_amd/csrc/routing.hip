@@ -195,11 +195,16 @@ __global__ __launch_bounds__(64) void route_rank_kernel(const int32_t* __restric
   }
 }
 
+// Row kernels launch one block per token and index rows with int32
+// positions: T and T*K must fit in 31 bits.
+inline bool rows_fit(int64_t T, int32_t K) { return T <= INT32_MAX / K; }
+
 int launch_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t src_const,
                  int32_t S, int32_t E, int64_t A, int32_t K, int32_t C, int32_t* phys,
                  int32_t* counts, int32_t* offsets, int32_t* pos, void* workspace,
                  size_t workspace_bytes, hipStream_t stream) {
   if (C <= 0 || C > kRouteMaxSlots || A < 0 || K <= 0) return PMX_ERR_ARG;
+  if (A > INT32_MAX) return PMX_ERR_SHAPE;  // positions and counts are int32
   if (!counts || !offsets || !workspace) return PMX_ERR_ARG;
   if (A > 0 && (!sel || !phys || !pos)) return PMX_ERR_ARG;
   if (M != nullptr && (S <= 0 || E <= 0)) return PMX_ERR_ARG;
@@ -524,6 +529,7 @@ int pmx_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t 
               pmx_stream_t stream) {
   if (T < 0 || K <= 0) return PMX_ERR_ARG;
   if (M == nullptr && src != nullptr) return PMX_ERR_ARG;
+  if (T > INT32_MAX / K) return PMX_ERR_SHAPE;
   return launch_route(sel, M, src, src_const, S, E, T * K, K, C, phys, counts, offsets, pos, workspace,
                       workspace_bytes, stream);
 }
@@ -538,6 +544,7 @@ int pmx_route_status(const void* workspace, int32_t* status_host, pmx_stream_t s
 int pmx_moe_scatter(const void* X, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* Xp,
                     pmx_stream_t stream) {
   if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
+  if (!rows_fit(T, K)) return PMX_ERR_SHAPE;
   if (T == 0 || H == 0) return PMX_OK;
   if (!X || !pos || !Xp) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
@@ -557,6 +564,7 @@ int pmx_moe_scatter(const void* X, const int32_t* pos, int64_t T, int32_t K, int
 int pmx_moe_gather(const void* Y, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* out,
                    pmx_stream_t stream) {
   if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
+  if (!rows_fit(T, K)) return PMX_ERR_SHAPE;
   if (T == 0 || H == 0) return PMX_OK;
   if (!Y || !pos || !out) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
@@ -577,6 +585,7 @@ int pmx_moe_gather(const void* Y, const int32_t* pos, int64_t T, int32_t K, int6
 int pmx_combine_fwd(const void* Y, const int32_t* pos, const void* w, int64_t T, int32_t K, int64_t H,
                     void* out, pmx_stream_t stream) {
   if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
+  if (!rows_fit(T, K)) return PMX_ERR_SHAPE;
   if (T == 0 || H == 0) return PMX_OK;
   if (!Y || !pos || !w || !out) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
@@ -598,6 +607,7 @@ int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const v
                     int32_t K, int64_t H, void* dY, void* dw, pmx_stream_t stream) {
   if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
   if (K > kMaxTopK) return PMX_ERR_ARG;
+  if (!rows_fit(T, K)) return PMX_ERR_SHAPE;
   if (T == 0) return PMX_OK;
   if (!dout || !Y || !pos || !w || !dY || !dw) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
@@ -630,7 +640,7 @@ int pmx_segment_sum(const void* source, const int64_t* index, int64_t N, int64_t
                     void* out, void* workspace, size_t workspace_bytes, pmx_stream_t stream) {
   if (N < 0 || H < 0 || num_rows < 0) return PMX_ERR_ARG;
   if (num_rows == 0) return N == 0 ? PMX_OK : PMX_ERR_ARG;
-  if (num_rows > kRouteMaxSlots) return PMX_ERR_SHAPE;
+  if (num_rows > kRouteMaxSlots || N > INT32_MAX) return PMX_ERR_SHAPE;
   if (!out || !workspace) return PMX_ERR_ARG;
   if (N > 0 && (!source || !index)) return PMX_ERR_ARG;
   if (workspace_bytes < pmx_segment_sum_workspace_bytes(N, num_rows)) return PMX_ERR_ARG;

@@ -70,3 +70,25 @@ def test_argument_errors_are_codes_not_crashes():
     assert lib.pmx_combine_bwd(None, None, None, None, 4, 33, 8, None, None, None) == _capi.PMX_ERR_ARG
     with pytest.raises(ValueError):
         _capi.call("pmx_group_gemm_nt", None, None, None, 4, 8, 12, 8, None, None)
+
+
+def test_size_limits_rejected_before_any_launch():
+    """Shapes beyond the 32-bit row and position indices are refused on the
+    host (PMX_ERR_SHAPE) before any HIP call, so this runs without a GPU."""
+    lib = _capi.load()
+    big = 1 << 31
+    dummy = ctypes.c_void_p(16)
+    ws = ctypes.c_void_p(16)
+    assert lib.pmx_moe_scatter(dummy, dummy, big, 1, 64, dummy, None) == _capi.PMX_ERR_SHAPE
+    assert lib.pmx_moe_gather(dummy, dummy, big // 8, 8, 64, dummy, None) == _capi.PMX_ERR_SHAPE
+    assert lib.pmx_combine_fwd(dummy, dummy, dummy, big, 1, 64, dummy, None) == _capi.PMX_ERR_SHAPE
+    assert lib.pmx_combine_bwd(dummy, dummy, dummy, dummy, big // 2, 2, 64, dummy, dummy, None) == _capi.PMX_ERR_SHAPE
+    assert lib.pmx_route(dummy, None, None, 0, 0, 0, big // 4, 4, 8, dummy, dummy, dummy, dummy, ws, 1 << 40,
+                         None) == _capi.PMX_ERR_SHAPE
+    assert lib.pmx_group_gemm_nt(dummy, dummy, dummy, 1, big, 64, 64, dummy, None) == _capi.PMX_ERR_SHAPE
+    # argument errors
+    assert lib.pmx_moe_scatter(dummy, dummy, -1, 1, 64, dummy, None) == _capi.PMX_ERR_ARG
+    assert lib.pmx_replica_exchange_pack(dummy, 7, 64, 4, 1, dummy, dummy, dummy, dummy, dummy, None) == \
+        _capi.PMX_ERR_ARG
+    assert lib.pmx_replica_exchange_unpack(dummy, 0, 64, 4, 1, dummy, dummy, 1, dummy, None, None, None, dummy,
+                                           None) == _capi.PMX_ERR_ARG
