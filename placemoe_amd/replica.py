@@ -175,7 +175,12 @@ class ReplicaGradExchange:
     -> ``owner_broadcast_finish(recv)``.  Sums are fp32 on the GPU, stored in
     the gradient dtype; every local copy ends with the expert's total."""
 
-    def __init__(self, schedule: ReplicaGradSchedule, ep_rank: int, grads: Sequence[torch.Tensor]):
+    def __init__(self, schedule: ReplicaGradSchedule, ep_rank: int, grads: Sequence[torch.Tensor],
+                 slot_tokens: torch.Tensor | None = None):
+        """``slot_tokens`` (tokens each local slot saw since the last sync):
+        slots with none are zeroed first, as ``_zero_inactive_slot_grads_for_layer``
+        (expert_swap.py:6250-6262) does; a count vector of the wrong length is
+        ignored, as there."""
         self.schedule = schedule
         self.ep_rank = int(ep_rank)
         self.grads = list(grads)
@@ -185,6 +190,13 @@ class ReplicaGradExchange:
             if g.dtype not in PMX_DTYPE:
                 raise ValueError(f"replica exchange supports bf16 and fp32 gradients, got {g.dtype}")
         self.device = self.grads[0].device
+        if slot_tokens is not None:
+            counts = torch.as_tensor(slot_tokens)
+            if counts.ndim == 1 and int(counts.numel()) == int(self.grads[0].shape[0]):
+                idle = torch.nonzero(counts.to(self.device) <= 0).flatten()
+                if idle.numel():
+                    for g in self.grads:
+                        g.index_fill_(0, idle, 0)
         self.numel = [int(g[0].numel()) if g.shape[0] else 0 for g in self.grads]
         self._status = torch.zeros(1, dtype=torch.int32, device=self.device)
         # Bytes the launched kernels must read and write (local copies, parts,

@@ -149,3 +149,27 @@ def test_bad_slot_sets_status():
     assert int(status.item()) == 1
     torch.testing.assert_close(out, before[1], rtol=0, atol=0)
     assert torch.equal(g, before)
+
+
+def test_inactive_slots_are_zeroed_first():
+    # _zero_inactive_slot_grads_for_layer (expert_swap.py:6250-6262): a copy
+    # that saw no tokens contributes nothing and then receives the total.
+    L, owners, nl = [0, 1, 0, 1], [0, 1], 2
+    cpu = fill_grads(L, nl, 2, value=lambda r, ls, e: (10.0 * (r + 1) + e, 100.0 * (r + 1) + e))
+    grads = to_dev(cpu, (torch.float32, torch.float32))
+    tokens = [torch.tensor([5, 0]), torch.tensor([3, 2])]  # rank 0's copy of expert 1 is idle
+    R = 2
+    ex = [ReplicaGradExchange(replica_grad_schedule(L, owners, nl, r, R), r, grads[r], slot_tokens=tokens[r])
+          for r in range(R)]
+    sends = [e.pairwise_send() for e in ex]
+    for r in range(R):
+        ex[r].pairwise_finish(hand_over(sends, r))
+    torch.cuda.synchronize()
+    for r in range(R):
+        assert torch.all(grads[r][0][0].cpu() == 10.0 + 20.0)        # expert 0: both copies active
+        assert torch.all(grads[r][0][1].cpu() == 21.0)               # expert 1: only rank 1's copy
+        assert torch.all(grads[r][1][1].cpu() == 201.0)
+    # a count vector of the wrong length is ignored, as in the reference
+    g2 = to_dev(cpu, (torch.float32, torch.float32))
+    ReplicaGradExchange(replica_grad_schedule(L, owners, nl, 0, R), 0, g2[0], slot_tokens=torch.tensor([0, 0, 0]))
+    torch.testing.assert_close(g2[0][0].cpu(), cpu[0][0], rtol=0, atol=0)
