@@ -272,6 +272,7 @@ class ReplicaGradExchange:
 
     def _check_status(self) -> None:
         if int(self._status.item()):
+            self._status.zero_()
             raise ValueError("replica exchange: a local slot lies outside the gradient tensor")
 
     def _pack(self, peer_groups: dict[int, list[ReplicaGradGroup]]) -> dict[torch.dtype, dict[int, torch.Tensor]]:
@@ -299,8 +300,9 @@ class ReplicaGradExchange:
                 need = sum(self.numel[p] for _ in groups for p in params)
                 if peer not in recv or int(recv[peer].numel()) < need:
                     raise ValueError(f"replica exchange: buffer from rank {peer} is missing or too short")
-                if recv[peer].dtype != dtype or recv[peer].device != self.device:
-                    raise ValueError("replica exchange: received buffer has the wrong dtype or device")
+                if recv[peer].dtype != dtype or recv[peer].device != self.device or not recv[peer].is_contiguous():
+                    raise ValueError("replica exchange: received buffer has the wrong dtype or device, "
+                                     "or is not contiguous")
             es = torch.empty((), dtype=dtype).element_size()
             if out_groups is not None:
                 o_off, o_sizes = self._layout(out_groups, params)
