@@ -117,6 +117,29 @@ def test_tn_wgrad_ragged_k_and_empty_groups(cuda, groups, M, N, split):
             assert torch.count_nonzero(c[gi]).item() == 0, "empty group must store zeros"
 
 
+def test_group_limit_mostly_empty(cuda):
+    # G = 2048 (the largest table the tile scheduler's prefix takes), a few
+    # hundred rows spread over a handful of groups: every other group is empty.
+    G = 2048
+    rng = np.random.default_rng(5)
+    counts = np.zeros(G, dtype=np.int64)
+    for gi, n in zip(rng.choice(G, 12, replace=False), rng.integers(1, 300, 12)):
+        counts[gi] = n
+    off = _offsets(counts)
+    A = int(off[-1])
+    g = torch.Generator().manual_seed(77)
+    a = torch.randn((A, 64), generator=g).to(torch.bfloat16)
+    b = (torch.randn((G, 72, 64), generator=g) * 0.05).to(torch.bfloat16)
+    print(f"nt G={G} A={A}", flush=True)
+    c = kernels.group_gemm_nt(a.to(cuda), b.to(cuda), _dev_offsets(off, cuda))
+    assert_bf16_close(c, O.grouped_gemm_nt(a, b, off), name="nt_g2048")
+    y = torch.randn((A, 40), generator=g).to(torch.bfloat16)
+    print(f"tn G={G} A={A}", flush=True)
+    w = kernels.group_gemm_tn(a.to(cuda), y.to(cuda), _dev_offsets(off, cuda))
+    assert_bf16_close(w, O.grouped_gemm_tn(a, y, off), name="tn_g2048")
+    assert torch.count_nonzero(w[torch.as_tensor(counts == 0)]).item() == 0
+
+
 def test_mfma_lane_layout_identity(cuda):
     # X @ I^T = X exactly: pins the MFMA output lane -> (row, col) mapping.
     A, H = 200, 128
