@@ -30,7 +30,7 @@ def offsets(counts, cuda):
     return off, torch.as_tensor(off, dtype=torch.int32).to(cuda)
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(24))
 def test_sweep_all_kinds(cuda, seed):
     rng, counts, (d0, d1, d2) = case(seed)
     off, doff = offsets(counts, cuda)

@@ -79,3 +79,27 @@ def test_combine_of_identity_routing_is_weighted_copy(cuda):
     pos = r.pos.cpu().numpy().reshape(-1)
     assert_exact(out, y[torch.as_tensor(pos)], "identity combine")
     assert np.array_equal(np.sort(pos), np.arange(T))
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_row_kernels_random_shapes(cuda, seed):
+    # Seeded sweep: top-k 1..8 (every K the kernels specialise on plus the
+    # generic path), H a multiple of 8 or not, copies 1..300.
+    rng = np.random.default_rng(500 + seed)
+    T = int(rng.integers(1, 700))
+    K = int(rng.integers(1, 9))
+    H = int(rng.choice([8, 24, 40, 264, 1000, 2056, 13, 77]))
+    C = int(rng.integers(1, 300))
+    print(f"rows seed={seed} T={T} K={K} H={H} C={C}", flush=True)
+    sel, y, w, dout = _inputs(T, K, H, C, seed)
+    x = torch.randn((T, H), generator=torch.Generator().manual_seed(seed)).to(torch.bfloat16)
+    r = kernels.route(sel.to(cuda), C)
+    pos = r.pos.cpu().numpy()
+    assert_exact(kernels.moe_scatter(x.to(cuda), r.pos), O.permute(x, pos), "scatter")
+    assert_bf16_close(kernels.combine_fwd(y.to(cuda), r.pos, w.to(cuda)), O.combine_forward(y, pos, w),
+                      name="combine out")
+    dy, dw = kernels.combine_bwd(dout.to(cuda), y.to(cuda), r.pos, w.to(cuda))
+    dy_ref, dw_ref = O.combine_backward(dout, y, pos, w)
+    assert_exact(dy, dy_ref, "combine dy")
+    assert_bf16_close(dw, dw_ref, name="combine dw")
+    assert_bf16_close(kernels.moe_gather(y.to(cuda), r.pos), O.unpermute_grad(y, pos), name="gather")
