@@ -23,7 +23,9 @@ def test_reference_known_answer(cuda):
 
 
 @pytest.mark.parametrize("seed,S,E,K,T", [(0, 2, 8, 2, 1000), (1, 8, 128, 8, 4096), (2, 16, 64, 4, 3000),
-                                          (3, 1, 3, 1, 17), (4, 4, 256, 32, 200)])
+                                          (3, 1, 3, 1, 17), (4, 4, 256, 32, 200),
+                                          # co-selection table in LDS: S*E*E <= 16384, many tokens per block
+                                          (5, 1, 128, 8, 20000), (6, 4, 64, 6, 2500), (7, 1, 2, 2, 9000)])
 def test_matches_oracle_over_samples(cuda, seed, S, E, K, T):
     print(f"stats seed={seed} S={S} E={E} K={K} T={T}", flush=True)
     g = torch.Generator().manual_seed(seed)
