@@ -133,3 +133,76 @@ def test_fused_moe_forward_public_op(cuda):
     phys = wl.selected.numpy()  # no placement registered: slot == expert id
     fwd = O.moe_layer_forward(wl.hidden, wl.routing_weights, phys, wl.fc1, wl.fc2)
     assert_bf16_close(out, fwd["out"], name="fused_moe_forward")
+
+
+def _eager_moe(num_experts, routing_weights, selected_experts, hidden, fc1_1, fc1_2, fc2):
+    """The reference test's per-expert loop (tests/ops/test_fused_moe_split_vs_merged.py:21-44),
+    run on the CPU in float32 (a reference for bf16 results)."""
+    out = torch.zeros_like(hidden)
+    mask = torch.nn.functional.one_hot(selected_experts, num_classes=num_experts).permute(2, 1, 0)
+    for e in torch.greater(mask.sum(dim=(-1, -2)), 0).nonzero():
+        idx = int(e[0])
+        top_k_pos, token_idx = torch.where(mask[idx])
+        x = hidden[token_idx]
+        gate = torch.nn.functional.linear(x, fc1_1[idx])
+        up = torch.nn.functional.linear(x, fc1_2[idx])
+        y = torch.nn.functional.linear(torch.nn.functional.silu(gate) * up, fc2[idx])
+        out.index_add_(0, token_idx, y * routing_weights[token_idx, top_k_pos, None])
+    return out
+
+
+@pytest.mark.parametrize("num_tokens,num_experts,hidden_dim,ffn_dim,topk,seed", [
+    (512, 128, 2048, 768, 8, 0),    # Qwen3-30B-A3B
+    (256, 64, 2048, 1408, 6, 1),    # Moonlight-16B-A3B
+])
+def test_reference_split_vs_merged_shapes(cuda, num_tokens, num_experts, hidden_dim, ffn_dim, topk, seed):
+    # tests/ops/test_fused_moe_split_vs_merged.py:45-161: the same inputs and
+    # checks, through the public op with the hip backend bound.
+    placemoe_amd.apply_veomni_fused_moe_patch("hip")
+    print(f"reference shape T={num_tokens} E={num_experts} H={hidden_dim} I={ffn_dim} k={topk}", flush=True)
+    torch.manual_seed(seed)
+    bf = torch.bfloat16
+    hidden = 0.1 * torch.randn(num_tokens, hidden_dim, dtype=bf)
+    logits = torch.randn(num_tokens, num_experts, dtype=torch.float32)
+    routing_weights, selected = torch.topk(torch.softmax(logits, dim=-1), topk, dim=-1)
+    routing_weights = routing_weights.to(bf)
+    fc1_1 = 0.1 * torch.randn(num_experts, ffn_dim, hidden_dim, dtype=bf)
+    fc1_2 = 0.1 * torch.randn(num_experts, ffn_dim, hidden_dim, dtype=bf)
+    fc1_12 = torch.cat([fc1_1, fc1_2], dim=1).contiguous()
+    fc2 = 0.1 * torch.randn(num_experts, hidden_dim, ffn_dim, dtype=bf)
+
+    def run(split):
+        hs = hidden.to(cuda).requires_grad_(True)
+        w2 = fc2.to(cuda).requires_grad_(True)
+        if split:
+            a, b = fc1_1.to(cuda).requires_grad_(True), fc1_2.to(cuda).requires_grad_(True)
+            out = placemoe_amd.fused_moe_forward(num_experts=num_experts, routing_weights=routing_weights.to(cuda),
+                                                 selected_experts=selected.to(cuda), hidden_states=hs,
+                                                 fc1_1_weight=a, fc1_2_weight=b, fc2_weight=w2)
+            out.sum().backward()
+            return out, hs.grad, w2.grad, torch.cat([a.grad, b.grad], dim=1)
+        w1 = fc1_12.to(cuda).requires_grad_(True)
+        out = placemoe_amd.fused_moe_forward(num_experts=num_experts, routing_weights=routing_weights.to(cuda),
+                                             selected_experts=selected.to(cuda), hidden_states=hs,
+                                             fc1_1_weight=None, fc1_2_weight=None, fc2_weight=w2,
+                                             fc1_1_2_weight=w1)
+        out.sum().backward()
+        return out, hs.grad, w2.grad, w1.grad
+
+    out_s, dh_s, dw2_s, dw1_s = (t.cpu() for t in run(True))
+    out_m, dh_m, dw2_m, dw1_m = (t.cpu() for t in run(False))
+    torch.testing.assert_close(out_s, out_m, rtol=0, atol=0)
+    torch.testing.assert_close(dh_s, dh_m, rtol=3e-2, atol=3e-2)
+    torch.testing.assert_close(dw2_s, dw2_m, rtol=0, atol=0)
+    torch.testing.assert_close(dw1_s, dw1_m, rtol=0, atol=0)
+
+    he = hidden.float().requires_grad_(True)
+    e1 = fc1_1.float().requires_grad_(True)
+    e2 = fc1_2.float().requires_grad_(True)
+    e3 = fc2.float().requires_grad_(True)
+    out_e = _eager_moe(num_experts, routing_weights.float(), selected, he, e1, e2, e3)
+    out_e.sum().backward()
+    torch.testing.assert_close(out_m.float(), out_e.detach(), rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(dh_m.float(), he.grad, rtol=5e-2, atol=5e-2)
+    torch.testing.assert_close(dw2_m.float(), e3.grad, rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(dw1_m.float(), torch.cat([e1.grad, e2.grad], dim=1), rtol=3e-2, atol=3e-2)
