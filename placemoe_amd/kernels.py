@@ -288,6 +288,11 @@ def group_gemm_tn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, split
     _bf16("b", b)
     M, N = a.shape[1], b.shape[1]
     G = offsets.numel() - 1
+    if a.shape[0] == 0:
+        # No rows at all (an empty micro-batch): every group is empty, so every C[g] is zero.
+        # The entry point takes non-null A and B, which an empty tensor does not have.
+        c = torch.zeros((G, M, N), dtype=a.dtype, device=dev)
+        return c if split is None else (c[:, :split].clone(), c[:, split:].clone())
     if split is None:
         c0 = torch.empty((G, M, N), dtype=a.dtype, device=dev)
         _capi.call(

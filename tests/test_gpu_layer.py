@@ -206,3 +206,20 @@ def test_reference_split_vs_merged_shapes(cuda, num_tokens, num_experts, hidden_
     torch.testing.assert_close(dh_m.float(), he.grad, rtol=5e-2, atol=5e-2)
     torch.testing.assert_close(dw2_m.float(), e3.grad, rtol=1e-2, atol=1e-2)
     torch.testing.assert_close(dw1_m.float(), torch.cat([e1.grad, e2.grad], dim=1), rtol=3e-2, atol=3e-2)
+
+
+def test_layer_with_no_tokens(cuda):
+    # An empty micro-batch: every kernel returns early; gradients are empty or zero.
+    wl = make_workload("qwen3", tokens=16)
+    H = wl.H
+    x = torch.zeros((0, H), dtype=torch.bfloat16, device=cuda, requires_grad=True)
+    w = torch.zeros((0, wl.K), dtype=torch.bfloat16, device=cuda, requires_grad=True)
+    sel = torch.zeros((0, wl.K), dtype=torch.int64, device=cuda)
+    fc1 = wl.fc1.to(cuda).requires_grad_(True)
+    fc2 = wl.fc2.to(cuda).requires_grad_(True)
+    out = experts.expert_layer(x, w, sel, fc2, fc1_1_2_weight=fc1, mapping=wl.mapping.to(cuda),
+                               sources=torch.zeros(0, dtype=torch.int64, device=cuda))
+    assert out.shape == (0, H)
+    out.backward(torch.zeros_like(out))
+    assert x.grad.shape == (0, H) and w.grad.shape == (0, wl.K)
+    assert torch.count_nonzero(fc1.grad).item() == 0 and torch.count_nonzero(fc2.grad).item() == 0
