@@ -20,8 +20,8 @@
 // instruction fetches one whole 128-byte line.  A block walks its tiles as one
 // stream of K-tiles, so the next tile's first loads overlap the current
 // tile's end and epilogue.  The loads are issued as inline asm, one every
-// other pinned MFMA group of the first two k-steps, and waited for by hand
-// (vmcnt).  Rows or columns outside a group, outside N/M, or past K are
+// other pinned MFMA group of the first two k-steps (one per group of the
+// first k-step for the wgrad), and waited for by hand (vmcnt).  Rows or columns outside a group, outside N/M, or past K are
 // masked by buffer range checks (an out-of-range offset loads zeros).
 //
 // LDS layouts, both XOR-swizzled in 16-byte chunks so that the fragment reads
@@ -691,8 +691,8 @@ __device__ __forceinline__ void block_barrier() {
 // Between barrier p-1 (after which stream K-tile p is in LDS and every wave
 // has finished reading K-tile p-1) and barrier p, a wave
 //   - issues its loads of K-tile p+1 into the stage of K-tile p-1, one per
-//     MFMA pair of the first two k-steps, so that they have the rest of the
-//     K-tile to land,
+//     MFMA pair of the first two k-steps (per MFMA of the first k-step for
+//     the wgrad), so that they have the rest of the K-tile to land,
 //   - multiplies the four 16-deep k-steps, reading each k-step's fragments
 //     during the previous k-step's MFMAs (k-step 0's during k-step 3 of
 //     K-tile p-1), so that LDS latency hides behind MFMAs,
@@ -806,8 +806,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
 
   // Per k-step: NM MFMAs, one per pinned group, and NR fragment reads, two
   // per group in the first groups.  The next K-tile's QA + QB loads go one
-  // every other group of the first two k-steps.
+  // every SPREAD-th group from the start of k-step 0: every other group of
+  // the first two k-steps, except for the wgrad, whose M/N-contiguous loads
+  // go one per group of k-step 0 (measured: +3% on the wgrad, 3-6% slower
+  // for the other kinds; spreading over three or four k-steps is slower).
   constexpr int NM = MT * NTT, NR = MT + NTT, PER = 1, NF = NM;
+  constexpr int SPREAD = KIND == KIND_TN ? 1 : 2;
   static_assert(NR % 2 == 0 && NR / 2 <= NF && QA + QB == NF, "schedule shape");
   f32x16_t acc[MT][NTT];
   Frags<BM> f0, f1;
@@ -831,7 +835,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       if constexpr (decltype(loads)::value) {
         static_for<0, QA + QB>([&](auto ll) __attribute__((always_inline)) {
           constexpr int l = decltype(ll)::value;
-          if constexpr (2 * l == decltype(ks)::value * NF + j) {
+          if constexpr (SPREAD * l == decltype(ks)::value * NF + j) {
             if constexpr (l < QA) issue_one<KIND, BM, 0, l>(refill, it, i_kt, i_live, wave);
             else issue_one<KIND, BM, 1, l - QA>(refill, it, i_kt, i_live, wave);
           }
