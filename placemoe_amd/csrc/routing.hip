@@ -25,12 +25,19 @@ struct RouteGeom {
   int64_t nchunks;  // number of chunks (>= 1)
 };
 
-RouteGeom route_geom(int64_t A) {
+// Chunks of 512 assignments (eight 64-wide wave segments), so that a
+// typical batch spreads over hundreds of one-wave blocks.  The chunk table
+// (nchunks x C int32) is capped at 2^24 entries and 1024 rows; past that the
+// chunks grow.
+RouteGeom route_geom(int64_t A, int32_t C) {
   RouteGeom g;
-  g.chunk = 2048;
+  int64_t max_chunks = (int64_t(1) << 24) / C;
+  if (max_chunks > 1024) max_chunks = 1024;
+  if (max_chunks < 1) max_chunks = 1;
+  g.chunk = 512;
   g.nchunks = (A + g.chunk - 1) / g.chunk;
-  if (g.nchunks > 256) {
-    int64_t per = (A + 255) / 256;
+  if (g.nchunks > max_chunks) {
+    const int64_t per = (A + max_chunks - 1) / max_chunks;
     g.chunk = (per + 63) / 64 * 64;
     g.nchunks = (A + g.chunk - 1) / g.chunk;
   }
@@ -40,13 +47,11 @@ RouteGeom route_geom(int64_t A) {
 
 constexpr size_t kStatusBytes = 256;
 
+// Workspace: the status word (256 B), the chunk table, then one flag per
+// chunk (its ids were clamped).
 size_t route_ws_bytes(int64_t A, int32_t C) {
-  RouteGeom g = route_geom(A);
-  return kStatusBytes + (size_t)g.nchunks * (size_t)C * sizeof(int32_t);
-}
-
-__global__ void route_status_clear_kernel(int32_t* status) {
-  if (threadIdx.x == 0) status[0] = 0;
+  RouteGeom g = route_geom(A, C);
+  return kStatusBytes + (size_t)g.nchunks * (size_t)C * sizeof(int32_t) + (size_t)g.nchunks * sizeof(int32_t);
 }
 
 // Device-side fill (kept off hipMemsetAsync so the path can sit in a graph).
@@ -62,7 +67,7 @@ template <bool USE_LDS>
 __global__ __launch_bounds__(64) void route_hist_kernel(
     const int64_t* __restrict__ sel, const int64_t* __restrict__ M, const int64_t* __restrict__ src,
     int32_t src_const, int32_t S, int32_t E, int32_t K, int32_t C, int64_t A, int64_t chunk,
-    int32_t* __restrict__ phys, int32_t* __restrict__ table, int32_t* __restrict__ status) {
+    int32_t* __restrict__ phys, int32_t* __restrict__ table, int32_t* __restrict__ flags) {
   extern __shared__ int32_t lds_hist[];
   const int lane = threadIdx.x;
   const int64_t ch = blockIdx.x;
@@ -92,33 +97,67 @@ __global__ __launch_bounds__(64) void route_hist_kernel(
   if (USE_LDS) {
     for (int c = lane; c < C; c += 64) row[c] = hist[c];
   }
-  if (bad) atomicOr(status, 1);
+  const bool any_bad = __ballot(bad) != 0;
+  if (lane == 0) flags[ch] = any_bad ? 1 : 0;
 }
 
-// Single block: column-wise exclusive scan of the chunk table (turning
-// histogram rows into per-chunk start positions), counts and offsets.
+// Single block: column-wise exclusive scan of the chunk table, turning
+// histogram rows into per-chunk start positions, plus counts, offsets and the
+// status word (the OR of the chunk flags).  With C < 1024 columns the 1024
+// threads split each column into P = 1024 / C row ranges: the ranges are
+// summed in parallel and their prefixes scanned in LDS, so a pass over the
+// table costs nchunks / P dependent rows instead of nchunks.
 __global__ __launch_bounds__(1024) void route_scan_kernel(int32_t* __restrict__ table, int64_t nchunks,
-                                                          int32_t C, int32_t* __restrict__ counts,
-                                                          int32_t* __restrict__ offsets) {
+                                                          int32_t C, const int32_t* __restrict__ flags,
+                                                          int32_t* __restrict__ counts,
+                                                          int32_t* __restrict__ offsets,
+                                                          int32_t* __restrict__ status) {
+  __shared__ int32_t part[1024];  // per (range, column): range sum, then range start
   __shared__ int32_t sums[1024];
   __shared__ int32_t carry_sh;
+  __shared__ int32_t bad_sh;
   const int tid = threadIdx.x;
-  for (int c = tid; c < C; c += 1024) {
+  const int W = C < 1024 ? C : 1024;  // columns per pass
+  int64_t P = 1024 / W;               // row ranges per column (1 when C >= 1024)
+  if (P > nchunks) P = nchunks;
+  const int64_t R = (nchunks + P - 1) / P;
+  const int64_t p = tid / W;
+  const int64_t r0 = p * R, r1 = r0 + R < nchunks ? r0 + R : nchunks;
+  const bool ranged = C < 1024;  // one pass covers every column; `part` holds range starts
+  if (tid == 0) bad_sh = 0;
+  __syncthreads();
+  {
+    int32_t b = 0;
+    for (int64_t r = tid; r < nchunks; r += 1024) b |= flags[r];
+    if (b) atomicOr(&bad_sh, 1);
+  }
+  // Totals per column (and per range).
+  for (int c0 = 0; c0 < C; c0 += W) {
+    const int c = c0 + tid % W;
     int32_t run = 0;
-    int64_t r = 0;
-    for (; r + 8 <= nchunks; r += 8) {
-      int32_t v[8];
+    if (p < P && c < C) {
+      int64_t r = r0;
+      for (; r + 8 <= r1; r += 8) {
+        int32_t v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = table[(r + j) * C + c];
+        for (int j = 0; j < 8; ++j) v[j] = table[(r + j) * C + c];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) { table[(r + j) * C + c] = run; run += v[j]; }
+        for (int j = 0; j < 8; ++j) run += v[j];
+      }
+      for (; r < r1; ++r) run += table[r * C + c];
     }
-    for (; r < nchunks; ++r) {
-      int32_t v = table[r * C + c];
-      table[r * C + c] = run;
-      run += v;
+    if (ranged) part[tid] = run;
+    else if (c < C) counts[c] = run;
+  }
+  __syncthreads();
+  if (ranged && tid < C) {
+    int32_t acc = 0;
+    for (int64_t q = 0; q < P; ++q) {
+      const int32_t v = part[q * W + tid];
+      part[q * W + tid] = acc;
+      acc += v;
     }
-    counts[c] = run;
+    counts[tid] = acc;
   }
   __syncthreads();
   if (tid == 0) carry_sh = 0;
@@ -142,10 +181,30 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(int32_t* __restrict__ 
   }
   if (tid == 0) offsets[C] = carry_sh;
   __syncthreads();
-  for (int c = tid; c < C; c += 1024) {
-    const int32_t o = offsets[c];
-    for (int64_t r = 0; r < nchunks; ++r) table[r * C + c] += o;
+  // Rows become start positions: offsets[c] + range start + running sum.
+  for (int c0 = 0; c0 < C; c0 += W) {
+    const int c = c0 + tid % W;
+    if (p < P && c < C) {
+      int32_t run = offsets[c] + (ranged ? part[tid] : 0);
+      int64_t r = r0;
+      for (; r + 8 <= r1; r += 8) {
+        int32_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = table[(r + j) * C + c];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          table[(r + j) * C + c] = run;
+          run += v[j];
+        }
+      }
+      for (; r < r1; ++r) {
+        const int32_t v = table[r * C + c];
+        table[r * C + c] = run;
+        run += v;
+      }
+    }
   }
+  if (tid == 0) status[0] = bad_sh;
 }
 
 // One wave per chunk: stable rank of every assignment among equal copies.
@@ -211,9 +270,8 @@ int launch_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32
   if (workspace_bytes < route_ws_bytes(A, C)) return PMX_ERR_ARG;
   int32_t* status = reinterpret_cast<int32_t*>(workspace);
   int32_t* table = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kStatusBytes);
-  RouteGeom g = route_geom(A);
-  route_status_clear_kernel<<<1, 64, 0, stream>>>(status);
-  PMX_LAUNCH_CHECK();
+  RouteGeom g = route_geom(A, C);
+  int32_t* flags = table + g.nchunks * (int64_t)C;
   const bool lds = C <= kRouteLdsMaxSlots;
   const size_t lds_bytes = lds ? (size_t)C * sizeof(int32_t) : 0;
   if (A == 0) {
@@ -222,13 +280,13 @@ int launch_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32
     fill_i32_kernel<<<(unsigned)((C + 255) / 256), 256, 0, stream>>>(table, C, 0);
   } else if (lds) {
     route_hist_kernel<true><<<(unsigned)g.nchunks, 64, lds_bytes, stream>>>(
-        sel, M, src, src_const, S, E, K, C, A, g.chunk, phys, table, status);
+        sel, M, src, src_const, S, E, K, C, A, g.chunk, phys, table, flags);
   } else {
     route_hist_kernel<false><<<(unsigned)g.nchunks, 64, 0, stream>>>(
-        sel, M, src, src_const, S, E, K, C, A, g.chunk, phys, table, status);
+        sel, M, src, src_const, S, E, K, C, A, g.chunk, phys, table, flags);
   }
   PMX_LAUNCH_CHECK();
-  route_scan_kernel<<<1, 1024, 0, stream>>>(table, g.nchunks, C, counts, offsets);
+  route_scan_kernel<<<1, 1024, 0, stream>>>(table, g.nchunks, C, flags, counts, offsets, status);
   PMX_LAUNCH_CHECK();
   if (A > 0) {
     int nbits = 1;

@@ -68,7 +68,8 @@ def test_route_reference_lut_known_answer(cuda):
 @pytest.mark.parametrize(
     "T,K,C,seed",
     [(1, 1, 1, 0), (1, 8, 3, 1), (63, 2, 5, 2), (64, 1, 7, 3), (65, 3, 9, 4), (2049, 2, 17, 5),
-     (3000, 8, 4096, 6), (700, 4, 9000, 7), (40000, 8, 160, 8), (70000, 8, 1, 9)],
+     (3000, 8, 4096, 6), (700, 4, 9000, 7), (40000, 8, 160, 8), (70000, 8, 1, 9),
+     (9000, 8, 1023, 10), (9000, 8, 1025, 11), (300000, 2, 37, 12)],
 )
 def test_route_identity_random_edges(cuda, T, K, C, seed):
     g = np.random.default_rng(seed)
@@ -95,6 +96,20 @@ def test_route_out_of_range_is_flagged_not_faulting(cuda):
     assert kernels.route_status(r) != 0
     pos = r.pos.cpu().numpy().reshape(-1)
     assert np.array_equal(np.sort(pos), np.arange(4))
+
+
+def test_route_flag_from_one_chunk_of_many(cuda):
+    # One id out of range deep inside a batch of hundreds of chunks: the
+    # status word is the OR over every chunk's flag.
+    g = np.random.default_rng(11)
+    sel = g.integers(0, 100, size=(20000, 8))
+    sel[15000, 3] = 100
+    r = kernels.route(torch.as_tensor(sel).to(cuda), 100)
+    assert kernels.route_status(r) != 0
+    pos = r.pos.cpu().numpy().reshape(-1)
+    assert np.array_equal(np.sort(pos), np.arange(pos.size))
+    sel[15000, 3] = 99
+    _check_route(cuda, sel, 100)
 
 
 @pytest.mark.parametrize("T,K,H", [(1, 1, 8), (37, 3, 1024), (513, 8, 2048), (100, 2, 7168), (31, 2, 13)])
