@@ -945,10 +945,10 @@ int grid_size() {
   return g_num_cus;
 }
 
-// 256 x 256 block tiles: a 32-deep K-tile (32 KB) feeds 2 MFLOP, half the
-// bytes per flop of 128 x 256 tiles; operand delivery from L2 is what bounds
-// this kernel, so that outweighs the coarser padding of ragged groups.  The
-// accumulators fill the 256 AGPRs.
+// 256 x 256 block tiles: a 64-deep K-tile (64 KB of operands) feeds 8.4
+// MFLOP, half the bytes per flop of 128 x 256 tiles; operand delivery is what
+// bounds this kernel, so that outweighs the coarser padding of ragged groups.
+// Each wave's 128 x 64 share takes 128 accumulator registers per lane.
 constexpr int kBM = 256;
 
 template <int KIND>
