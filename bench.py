@@ -161,6 +161,26 @@ def cpu_baseline(wl, sample_tokens: int, backward: bool):
     return {"value": value, "unit": "ms", "cores": threads, "kind": "port", "sample": sample}
 
 
+def device_copy_gbps(dev, reps: int = 10) -> float:
+    """Read+write rate of a plain 1 GiB device-to-device copy (torch `copy_`)
+    on this box, timed with HIP events: the practical streaming ceiling that
+    the row-movement kernels are compared with, beside the 8 TB/s peak."""
+    x = torch.empty(2**29, dtype=torch.bfloat16, device=dev)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        y.copy_(x)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    del x, y
+    return round(2 * 2**30 / (ms * 1e-3) / 1e9, 1)
+
+
 def aux_measurements(wl, dev, reps: int = 10):
     """Kernels beside the layer step, timed with HIP events around direct
     C-ABI calls (preallocated buffers, no host synchronisation inside):
@@ -476,6 +496,7 @@ def main():
     result["aux_kernel_ms"] = aux_ms
     result["aux_bandwidth_gbps"] = aux_bw
     result["aux_config"] = aux_cfg
+    result["device_copy_gbps"] = device_copy_gbps(dev)
     if args.vendor_gemm:
         result["vendor_gemm"] = vendor_gemms(wl, dev)
     if not args.no_cpu_baseline:
