@@ -162,9 +162,9 @@ def cpu_baseline(wl, sample_tokens: int, backward: bool):
 
 
 def device_copy_gbps(dev, reps: int = 10) -> float:
-    """Read+write rate of a plain 1 GiB device-to-device copy (torch `copy_`)
-    on this box, timed with HIP events: the practical streaming ceiling that
-    the row-movement kernels are compared with, beside the 8 TB/s peak."""
+    """Read+write rate of a plain 1 GiB device-to-device copy (torch `copy_`,
+    ROCm's blit kernel) on this box, timed with HIP events: a reference point
+    for the box's streaming rate beside the 8 TB/s peak."""
     x = torch.empty(2**29, dtype=torch.bfloat16, device=dev)
     y = torch.empty_like(x)
     y.copy_(x)
