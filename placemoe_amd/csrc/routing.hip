@@ -318,10 +318,11 @@ int launch_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32
     default: LAUNCH(0); break;    \
   }
 
-// One thread per 16-byte chunk of a row, whole waves, at most 256 threads:
-// short blocks keep many rows in flight per CU (measured faster than one
-// thread per chunk of rows up to 7168 bf16 with 1024-thread blocks).
-constexpr int kRowThreads = 256;
+// One thread per 16-byte chunk of a row, whole waves, at most 512 threads:
+// short blocks keep many rows in flight per CU (1024-thread blocks were
+// slower on rows of 7168 bf16; there 384-512 threads gathered 7% faster than
+// 256 and the other row kernels ran equal).
+constexpr int kRowThreads = 512;
 inline unsigned row_threads(int64_t H) {
   int64_t v = (H + 7) / 8;
   v = (v + 63) / 64 * 64;
