@@ -36,6 +36,24 @@ def test_matches_oracle_over_samples(cuda, seed, S, E, K, T):
     np.testing.assert_array_equal(stats.affinity, affinity)
 
 
+@pytest.mark.parametrize("seed,S,E,K,T", [(8, 8, 128, 8, 6000), (9, 2, 96, 6, 5000)])
+def test_skewed_routing_with_repeats_matches_oracle(cuda, seed, S, E, K, T):
+    # Global co-selection table (S*E*E > 16384) under heavy skew: most picks
+    # fall on four experts, so many lanes of a wave hold the same pair, and
+    # repeated experts inside a token (ea == eb) add nothing.
+    print(f"stats skewed seed={seed} S={S} E={E} K={K} T={T}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    def draw(n):
+        hot = torch.randint(0, 4, (n, K), generator=g)
+        cold = torch.randint(0, E, (n, K), generator=g)
+        return torch.where(torch.rand((n, K), generator=g) < 0.85, hot, cold)
+    samples = [[draw(T + 5 * s) for s in range(S)]]
+    stats = profile_route_statistics([[r.to(cuda) for r in smp] for smp in samples], num_experts=E)
+    demand, affinity = O.route_statistics([[r.numpy() for r in smp] for smp in samples], E)
+    np.testing.assert_array_equal(stats.demand, demand)
+    np.testing.assert_array_equal(stats.affinity, affinity)
+
+
 def test_per_token_sources_match_split_by_source(cuda):
     wl = make_workload("qwen3", device=cuda, weights=False)
     rec = RouteStatisticsRecorder(8, wl.num_experts)
