@@ -157,9 +157,10 @@ int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_c
 /* dgrad fc2 followed by the SwiGLU backward:
  *   dact = bf16(dY[a] @ down[g])                      ([A,I])
  *   dG1[a, 0:I] = d_gate, dG1[a, I:2I] = d_up         (silu_backward rounding)
- * dY [A,H], down [G,H,I], gu [A,2I] from the forward, dG1 [A,2I].  Two
- * launches on `stream`: the GEMM leaves dact in dG1[a, I:2I], then an
- * elementwise pass rewrites both halves in place (no workspace).
+ * dY [A,H], down [G,H,I], gu [A,2I] from the forward, dG1 [A,2I].  One
+ * launch on `stream`: the GEMM's epilogue rounds dact to bf16, reads the
+ * rows' gate/up and writes both halves of dG1 (no workspace; dact is never
+ * stored).
  * Replaces the dgrad + silu_backward + cat of EPMergedFc1GroupGemm.backward
  * (veomni/distributed/moe/moe_layer.py:453-482). */
 int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void* gu,

@@ -3,7 +3,8 @@
 // One persistent kernel template serves every GEMM of the layer:
 //   KIND_FC1   X[a] @ [Wgate;Wup][g]^T with the SwiGLU forward epilogue
 //   KIND_NT    A[a] @ B[g]^T                       (fc2 forward)
-//   KIND_NN    A[a] @ B[g]                         (fc1 and fc2 dgrad)
+//   KIND_NN    A[a] @ B[g]                         (fc1 dgrad)
+//   KIND_NNS   A[a] @ B[g] with the SwiGLU backward epilogue (fc2 dgrad)
 //   KIND_TN    A[rows g]^T @ B[rows g]             (wgrad, ragged K)
 // Groups are the per-copy row ranges [offsets[g], offsets[g+1]).  A grid of
 // one block per CU walks a tile list derived on the device from `offsets`,
@@ -57,7 +58,7 @@ constexpr int kMaxGroups = 2048;
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always fails the range check
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
-enum Kind { KIND_FC1 = 0, KIND_NT = 1, KIND_NN = 2, KIND_TN = 4 };
+enum Kind { KIND_FC1 = 0, KIND_NT = 1, KIND_NN = 2, KIND_NNS = 3, KIND_TN = 4 };
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 #define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
@@ -78,18 +79,19 @@ struct GemmParams {
   const int32_t* offsets;
   int32_t G;
   int64_t M, N, K;  // ragged-M kinds: N, K used.  KIND_TN: M, N used.
-  int64_t I;        // SwiGLU width for KIND_FC1
+  int64_t I;        // SwiGLU width for KIND_FC1 and KIND_NNS
   bf16_t* c0;
   bf16_t* c1;
   int64_t ldc, cgs, csplit;
   bf16_t* gu;  // written by KIND_FC1
   bf16_t* act;
+  const bf16_t* gin;  // KIND_NNS: the forward's gate/up rows [A, 2I]
 };
 
 template <int KIND>
 constexpr bool a_is_mn() { return KIND == KIND_TN; }
 template <int KIND>
-constexpr bool b_is_mn() { return KIND == KIND_NN || KIND == KIND_TN; }
+constexpr bool b_is_mn() { return KIND == KIND_NN || KIND == KIND_NNS || KIND == KIND_TN; }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
   const uint32_t n = bytes > 0x7fffffffull ? 0x7fffffffu : (uint32_t)bytes;
@@ -379,6 +381,22 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[MT][NTT]) {
 // wave issues its next loads.  Rows of a round are 128 bytes; 16-byte chunk c
 // of row r sits at c ^ ((r >> 1) & 7).
 
+// SwiGLU backward of 8 columns, with the reference's rounding points
+// (swiglu_backward of its group GEMM path): dact is the bf16 dgrad output,
+//   s = bf16(silu(g)), d_silu = bf16(dact * u), sig = sigmoid(g)
+//   dgate = d_silu * sig * (1 + g * (1 - sig)),  dup = s * dact.
+__device__ __forceinline__ void swiglu_bwd8(const float* dact, const float* g, const float* u, float* dgate,
+                                            float* dup) {
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const float s = round_bf16(silu_f32(g[q]));
+    const float d_silu = round_bf16(dact[q] * u[q]);
+    const float sig = sigmoid_f32(g[q]);
+    dgate[q] = d_silu * (sig * (1.0f + g[q] * (1.0f - sig)));
+    dup[q] = s * dact[q];
+  }
+}
+
 __device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
   return make_uint2(f32_to_bf16(a) | (f32_to_bf16(b) << 16), f32_to_bf16(c) | (f32_to_bf16(d) << 16));
 }
@@ -448,6 +466,41 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
         const uint4 v = staged_chunk(stage, wave, rl, c4);
         const int64_t j = j0 + c4 * 8;
         if (row < ti.row_end && j < I) *reinterpret_cast<uint4*>(P.act + row * I + j) = v;
+      }
+    } else if constexpr (KIND == KIND_NNS) {
+      // fc2 dgrad: the tile is dact (bf16, as the reference stores it) for
+      // columns j < I; with the forward's gate/up of the same rows it becomes
+      // [d_gate | d_up] of dG1.  The round's gate/up loads go out first, so
+      // that their latency overlaps the staging.
+      const int64_t I = P.I;
+      const int cc = lane & 7;
+      const int64_t j = (int64_t)ti.ntile * BN + wn * WCOLS + cc * 8;
+      uint4 gv[8], uv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int64_t row = ti.row0 + rb + q * 8 + (lane >> 3);
+        if (row < ti.row_end && j < I) {
+          gv[q] = ld_stream(P.gin + row * 2 * I + j);
+          uv[q] = ld_stream(P.gin + row * 2 * I + I + j);
+        } else {
+          gv[q] = uv[q] = make_uint4(0u, 0u, 0u, 0u);
+        }
+      }
+      stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int rl = q * 8 + (lane >> 3);
+        const int64_t row = ti.row0 + rb + rl;
+        const uint4 v = staged_chunk(stage, wave, rl, cc);
+        if (row < ti.row_end && j < I) {
+          float d[8], g[8], u[8], dg[8], du[8];
+          unpack8(v, d);
+          unpack8(gv[q], g);
+          unpack8(uv[q], u);
+          swiglu_bwd8(d, g, u, dg, du);
+          *reinterpret_cast<uint4*>(P.c0 + row * 2 * I + j) = pack8(dg);
+          *reinterpret_cast<uint4*>(P.c0 + row * 2 * I + I + j) = pack8(du);
+        }
       }
     } else {
       stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
@@ -903,35 +956,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   }
 }
 
-// SwiGLU backward of fc2's dgrad, 8 columns per thread.  dG1 row r holds
-// dact in its up half on entry; gate/up are gu's halves.  Per element
-//   s = bf16(silu(g)), d_silu = bf16(dact * u), sig = sigmoid(g)
-//   dG1[gate] = d_silu * sig * (1 + g * (1 - sig)),  dG1[up] = s * dact
-// (swiglu_backward of the reference's group GEMM path; each thread reads the
-// dact chunk it then overwrites).
-__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const bf16_t* __restrict__ gu, bf16_t* dg1, uint32_t chunks,
-                                                         uint32_t total, int64_t ld) {
-  for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < total; e += gridDim.x * 256u) {
-    const uint32_t r = e / chunks;
-    const int64_t c = (int64_t)(e - r * chunks) * 8;
-    const int64_t row = (int64_t)r * ld, up = ld / 2;
-    float dact[8], g[8], u[8], dgate[8], dup[8];
-    unpack8(ld_stream(dg1 + row + up + c), dact);
-    unpack8(ld_stream(gu + row + c), g);
-    unpack8(ld_stream(gu + row + up + c), u);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const float s = round_bf16(silu_f32(g[q]));
-      const float d_silu = round_bf16(dact[q] * u[q]);
-      const float sig = sigmoid_f32(g[q]);
-      dgate[q] = d_silu * (sig * (1.0f + g[q] * (1.0f - sig)));
-      dup[q] = s * dact[q];
-    }
-    *reinterpret_cast<uint4*>(dg1 + row + c) = pack8(dgate);
-    *reinterpret_cast<uint4*>(dg1 + row + up + c) = pack8(dup);
-  }
-}
-
 int g_num_cus = 0;
 
 int grid_size() {
@@ -1059,8 +1083,7 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
   if (!dY || !w_down || !gu || !offsets || !dG1) return PMX_ERR_ARG;
   if (!a16(dY) || !a16(w_down) || !a16(gu) || !a16(dG1)) return PMX_ERR_SHAPE;
   if (!fits_rsrc(H, I) || !fits_rsrc(kBM, H)) return PMX_ERR_SHAPE;
-  if (A * (I / 8) > (int64_t)UINT32_MAX) return PMX_ERR_SHAPE;
-  // dact = dY @ Wdown[g] (bf16), written into the up half of dG1's rows ...
+  // dact = dY @ Wdown[g], finished in the epilogue: dG1 = [d_gate | d_up].
   GemmParams P = {};
   P.a = one(dY, 0, H);
   P.b = one(w_down, H * I, I);
@@ -1068,17 +1091,11 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
   P.G = G;
   P.N = I;
   P.K = H;
-  P.c0 = static_cast<bf16_t*>(dG1) + I;
+  P.I = I;
+  P.c0 = static_cast<bf16_t*>(dG1);
   P.ldc = 2 * I;
-  const int rc = launch<KIND_NN>(P, stream);
-  if (rc != PMX_OK) return rc;
-  // ... then the SwiGLU backward in place.
-  const uint32_t chunks = (uint32_t)(I / 8), total = (uint32_t)(A * (I / 8));
-  const uint32_t blocks = (total + 255) / 256 < 4096u ? (total + 255) / 256 : 4096u;
-  swiglu_bwd_kernel<<<blocks, 256, 0, stream>>>(static_cast<const bf16_t*>(gu), static_cast<bf16_t*>(dG1), chunks,
-                                                total, 2 * I);
-  PMX_LAUNCH_CHECK();
-  return PMX_OK;
+  P.gin = static_cast<const bf16_t*>(gu);
+  return launch<KIND_NNS>(P, stream);
 }
 
 int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
