@@ -171,6 +171,9 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
  *   C[g] = bf16(A[rows of g]^T @ B[rows of g]),  A [rows,M], B [rows,N], C [G,M,N];
  * a group with no rows stores zeros.  Rows m >= c_split of C[g] go to C1
  * (split fc1 gradients), else to C0; pass C1 = NULL for one tensor.
+ * A and B must be valid device pointers even when every group is empty
+ * (PMX_ERR_ARG otherwise); with no rows at all the caller can skip the call,
+ * since every C[g] is zero.
  * Replaces group_gemm_same_mn(transpose_a=True)
  * (veomni/ops/kernels/moe/_kernels/kernel/group_gemm.py:370-410). */
 int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int32_t G,
