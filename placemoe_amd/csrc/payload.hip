@@ -90,11 +90,14 @@ __global__ __launch_bounds__(256) void payload_rows_kernel(const bf16_t* __restr
   const int64_t t = blockIdx.x;
   const int64_t n8 = H / 8;
   const uint4* src = reinterpret_cast<const uint4*>(hidden + t * H);
-  for (int k = 0; k < K; ++k) {
-    const int64_t a = t * K + k;
-    if (first_rank[a] == R) continue;
-    uint4* dst = reinterpret_cast<uint4*>(send_hidden + (int64_t)upos[a] * H);
-    for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) dst[i] = ld_stream(src + i);
+  // The row is read once per chunk and stored to every rank that takes it.
+  for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
+    const uint4 v = ld_stream(src + i);
+    for (int k = 0; k < K; ++k) {
+      const int64_t a = t * K + k;
+      if (first_rank[a] == R) continue;
+      reinterpret_cast<uint4*>(send_hidden + (int64_t)upos[a] * H)[i] = v;
+    }
   }
 }
 
