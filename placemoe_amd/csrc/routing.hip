@@ -420,8 +420,8 @@ __global__ __launch_bounds__(kRowThreads) void gather_rows_kernel(const bf16_t* 
 
 // KC > 0: K == KC at compile time; a chunk's K loads of Y are issued together.
 // Top-1 (KC == 1) stores dY with streaming stores (see st_row).  dout and Y
-// are read with plain loads: measured 1.5-3% faster than streaming loads here
-// (top-1 and top-8), while the gathers lose 8-14% with plain loads.
+// are read with streaming loads: plain loads measured 1.5-3% faster on
+// isolated buffers but 11% slower inside the layer step (Qwen3 shape).
 template <bool VEC, int KC = 0>
 __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* __restrict__ dout,
                                                            const bf16_t* __restrict__ Y,
@@ -446,10 +446,10 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* 
     }
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       float d[8];
-      unpack8(*(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
+      unpack8(ld_stream(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
       uint4 yv[KC];
 #pragma unroll
-      for (int k = 0; k < KC; ++k) yv[k] = *(reinterpret_cast<const uint4*>(Y + rows[k]) + i);
+      for (int k = 0; k < KC; ++k) yv[k] = ld_stream(reinterpret_cast<const uint4*>(Y + rows[k]) + i);
 #pragma unroll
       for (int k = 0; k < KC; ++k) {
         float g[8], y[8];
@@ -467,7 +467,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* 
     const int64_t n8 = H / 8;
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       float d[8];
-      unpack8(*(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
+      unpack8(ld_stream(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
 #pragma unroll
       for (int k = 0; k < kMaxTopK; ++k) {
         if (k < K) {
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* 
 #pragma unroll
           for (int j = 0; j < 8; ++j) g[j] = d[j] * wk;
           reinterpret_cast<uint4*>(dY + row * H)[i] = pack8(g);
-          unpack8(*(reinterpret_cast<const uint4*>(Y + row * H) + i), y);
+          unpack8(ld_stream(reinterpret_cast<const uint4*>(Y + row * H) + i), y);
           float s = 0.f;
 #pragma unroll
           for (int j = 0; j < 8; ++j) s += round_bf16(d[j] * y[j]);
