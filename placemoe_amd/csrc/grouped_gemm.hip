@@ -382,7 +382,9 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[MT][NTT]) {
 // of row r sits at c ^ ((r >> 1) & 7).
 
 // SwiGLU backward of 8 columns, with the reference's rounding points
-// (swiglu_backward of its group GEMM path): dact is the bf16 dgrad output,
+// (aten silu_backward and the products around it in
+// EPMergedFc1GroupGemm.backward, veomni/distributed/moe/moe_layer.py:453-482,
+// :479): dact is the bf16 dgrad output,
 //   s = bf16(silu(g)), d_silu = bf16(dact * u), sig = sigmoid(g)
 //   dgate = d_silu * sig * (1 + g * (1 - sig)),  dup = s * dact.
 __device__ __forceinline__ void swiglu_bwd8(const float* dact, const float* g, const float* u, float* dgate,
