@@ -6,10 +6,12 @@ SwiGLU -> fc2 -> weighted combine, then the backward (combine gradient, fc2
 dgrad + SwiGLU backward, fc2 and fc1 wgrad, fc1 dgrad, unpermute gradient).
 Inputs and weights are resident in HBM before the timed region starts.
 
-Default workload: BASELINE config 2 (Qwen3-30B-A3B shape: T=16384, H=2048,
-E=128 -> C=160 copies, top-8, I=768, 8 sources).  ``--config`` picks another;
-``--config fold`` (config 5) adds the replica-gradient fold of both copy
-gradients (fp32 logical sums, written back to every copy) to each step.
+Default workload: the DeepSeek-V3-shape share of one EP rank (65536 received
+rows, H=7168, I=2048, 16 physical slots with Zipf(1.0) row counts, fwd+bwd):
+the configuration the grouped-GEMM target is quoted on and the largest that
+fits one GPU.  ``--config`` picks another; ``--config fold`` adds the
+replica-gradient fold of both copy gradients (fp32 logical sums, written back
+to every copy) to each step.
 
 Prints ONE JSON line.  ``value`` is the layer fwd+bwd time in ms (lower is
 better); the grouped-GEMM TFLOP/s and permute GB/s of the same run, the
@@ -97,12 +99,13 @@ class EventTimer:
 def parse():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--config", default="qwen3", choices=["toy", "qwen3", "dsv3", "skew", "fold"])
-    p.add_argument("--cpu-sample-tokens", type=int, default=1024)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--config", default="dsv3", choices=["toy", "qwen3", "dsv3", "skew", "fold"])
+    p.add_argument("--cpu-sample-tokens", type=int, default=None,
+                   help="tokens of the CPU baseline's sample (default: 1/16 of the batch, at least 1024)")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--profile-steps", type=int, default=5, help="extra steps timed per kernel with HIP events")
+    p.add_argument("--profile-steps", type=int, default=20, help="extra steps timed per kernel with HIP events")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="first run a plain 1 GiB device copy (reference kernel for HBM-traffic counters)")
     p.add_argument("--vendor-gemm", action="store_true",
@@ -110,13 +113,40 @@ def parse():
     return p.parse_args()
 
 
-def cpu_baseline(wl, sample_tokens: int, backward: bool):
+def host_cpu() -> dict:
+    """The host's CPU model, its logical CPU count, the CPUs this process may
+    run on, and the CPU threads the job is given (OMP_NUM_THREADS, which the
+    GPU pool sets to its per-GPU share of the host)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = os.cpu_count() or 1
+    share = os.environ.get("OMP_NUM_THREADS")
+    threads = int(share) if share and share.isdigit() and int(share) > 0 else affinity
+    return {"model": model, "cpu_count": os.cpu_count(), "affinity": affinity,
+            "threads": min(threads, affinity)}
+
+
+def cpu_baseline(wl, sample_tokens: int | None, backward: bool):
     """The CPU oracle (torch on the host cores) on the first ``sample_tokens``
-    tokens of the same workload, scaled linearly to the full token count."""
+    tokens of the same workload, scaled linearly to the full token count.
+    Runs on every CPU thread the job is given (``host_cpu()['threads']``)."""
     from oracle import moe_oracle as O
 
-    threads = min(os.cpu_count() or 1, 16)
+    host = host_cpu()
+    threads = host["threads"]
     torch.set_num_threads(threads)
+    if sample_tokens is None:
+        sample_tokens = max(1024, wl.T // 16)
     Ts = min(sample_tokens, wl.T)
     x = wl.hidden[:Ts].cpu()
     w = wl.routing_weights[:Ts].cpu()
@@ -158,7 +188,10 @@ def cpu_baseline(wl, sample_tokens: int, backward: bool):
         sample += (f"; plus the oracle replica fold of both copy gradients over the {picked.size} copies of "
                    f"{fold_experts} experts ({fold_ms:.1f} ms), scaled x{L.size / picked.size:g} to all "
                    f"{L.size} copies")
-    return {"value": value, "unit": "ms", "cores": threads, "kind": "port", "sample": sample}
+    sample += (f"; {threads} torch threads on {host['model']} (host: {host['cpu_count']} logical CPUs, "
+               f"{host['affinity']} in this process's affinity set)")
+    return {"value": value, "unit": "ms", "cores": threads, "kind": "port", "sample": sample,
+            "cpu_model": host["model"], "host_cpu_count": host["cpu_count"], "affinity_cpus": host["affinity"]}
 
 
 def device_copy_gbps(dev, reps: int = 10) -> float:

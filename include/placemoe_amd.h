@@ -189,12 +189,14 @@ int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int3
  * grads: bf16 [C,P]; out: fp32 [E,P]; slot_tokens: int64 [C] tokens seen by
  * each copy, or NULL to treat every copy as active.  If writeback != 0 every
  * copy of e (active or not) is overwritten with bf16(out[e]).
+ * A copy_slots entry outside [0, C) is neither read nor written and sets
+ * *status (device int32, caller-zeroed; may be NULL) to 1.
  * Replaces _zero_inactive_slot_grads_for_layer (expert_swap.py:6250-6262),
  * _replica_grad_contributions (:6839-6876) and _unpack_replica_grad
  * (:6886-6889) for the copies held by one GPU. */
 int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const int32_t* copy_slots,
                      const int64_t* slot_tokens, int32_t E, int32_t C, int64_t P, float* out,
-                     int32_t writeback, pmx_stream_t stream);
+                     int32_t writeback, int32_t* status, pmx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Cross-rank replica-gradient exchange: the per-rank halves                 */

@@ -73,7 +73,7 @@ SIGNATURES = {
     "pmx_replica_fold": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, POINTER(c_float), c_int32,
-         c_void_p],
+         c_void_p, c_void_p],
     ),
     "pmx_replica_exchange_pack": (
         c_int,

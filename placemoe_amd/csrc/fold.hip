@@ -11,16 +11,24 @@ template <bool VEC>
 __global__ __launch_bounds__(256) void replica_fold_kernel(bf16_t* __restrict__ grads,
                                                            const int32_t* __restrict__ copy_offsets,
                                                            const int32_t* __restrict__ copy_slots,
-                                                           const int64_t* __restrict__ slot_tokens, int64_t P,
-                                                           float* __restrict__ out, int writeback) {
+                                                           const int64_t* __restrict__ slot_tokens, int32_t C,
+                                                           int64_t P, float* __restrict__ out, int writeback,
+                                                           int32_t* __restrict__ status) {
   const int64_t e = blockIdx.y;
   const int32_t b = copy_offsets[e], end = copy_offsets[e + 1];
+  // A copy-table entry outside [0, C) is skipped in both the sum and the
+  // write-back and flagged once, by the expert's first block.
+  bool bad = false;
   if (VEC) {
     const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
     if (i >= P) return;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int32_t j = b; j < end; ++j) {
       const int64_t c = copy_slots[j];
+      if (c < 0 || c >= C) {
+        bad = true;
+        continue;
+      }
       if (slot_tokens != nullptr && slot_tokens[c] <= 0) continue;
       float f[8];
       unpack8(ld_stream(grads + c * P + i), f);
@@ -32,7 +40,10 @@ __global__ __launch_bounds__(256) void replica_fold_kernel(bf16_t* __restrict__ 
     o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
     if (writeback) {
       const uint4 v = pack8(acc);
-      for (int32_t j = b; j < end; ++j) *reinterpret_cast<uint4*>(grads + (int64_t)copy_slots[j] * P + i) = v;
+      for (int32_t j = b; j < end; ++j) {
+        const int64_t c = copy_slots[j];
+        if (c >= 0 && c < C) *reinterpret_cast<uint4*>(grads + c * P + i) = v;
+      }
     }
   } else {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -40,22 +51,30 @@ __global__ __launch_bounds__(256) void replica_fold_kernel(bf16_t* __restrict__ 
     float acc = 0.f;
     for (int32_t j = b; j < end; ++j) {
       const int64_t c = copy_slots[j];
+      if (c < 0 || c >= C) {
+        bad = true;
+        continue;
+      }
       if (slot_tokens != nullptr && slot_tokens[c] <= 0) continue;
       acc += bf16_to_f32(grads[c * P + i]);
     }
     out[e * P + i] = acc;
     if (writeback) {
       const bf16_t v = (bf16_t)f32_to_bf16(acc);
-      for (int32_t j = b; j < end; ++j) grads[(int64_t)copy_slots[j] * P + i] = v;
+      for (int32_t j = b; j < end; ++j) {
+        const int64_t c = copy_slots[j];
+        if (c >= 0 && c < C) grads[c * P + i] = v;
+      }
     }
   }
+  if (bad && status != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *status = 1;
 }
 
 }  // namespace
 
 extern "C" int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const int32_t* copy_slots,
                                 const int64_t* slot_tokens, int32_t E, int32_t C, int64_t P, float* out,
-                                int32_t writeback, pmx_stream_t stream) {
+                                int32_t writeback, int32_t* status, pmx_stream_t stream) {
   if (E <= 0 || C <= 0 || P < 0 || E > 65535) return PMX_ERR_ARG;
   if (P == 0) return PMX_OK;
   if (!grads || !copy_offsets || !copy_slots || !out) return PMX_ERR_ARG;
@@ -67,10 +86,10 @@ extern "C" int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const 
   dim3 grid((unsigned)gx, (unsigned)E);
   if (vec) {
     replica_fold_kernel<true><<<grid, 256, 0, stream>>>(static_cast<bf16_t*>(grads), copy_offsets, copy_slots,
-                                                       slot_tokens, P, out, writeback);
+                                                       slot_tokens, C, P, out, writeback, status);
   } else {
     replica_fold_kernel<false><<<grid, 256, 0, stream>>>(static_cast<bf16_t*>(grads), copy_offsets, copy_slots,
-                                                        slot_tokens, P, out, writeback);
+                                                        slot_tokens, C, P, out, writeback, status);
   }
   PMX_LAUNCH_CHECK();
   return PMX_OK;

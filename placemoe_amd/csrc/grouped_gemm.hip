@@ -35,6 +35,7 @@
 //     ds_read_b64_tr_b16, which transpose 4x16 blocks on the way out of LDS.
 
 #include "common.h"
+#include "ktile.h"
 
 namespace {
 
@@ -115,7 +116,7 @@ struct Operand {
   __amdgpu_buffer_rsrc_t r0, r1;  // K-contiguous: r1 holds fc1's up rows;
                                   // MN weights: k-rows below / from `split`
   const char* base;               // wgrad operands: the group's first row ...
-  uint32_t bytes;                 // ... and the bytes of its rows (descriptor rebased per K-tile)
+  uint64_t bytes;                 // ... and the bytes of its rows (descriptor rebased per K-tile)
   uint32_t ldb;                   // bytes between consecutive (k-)rows
   int32_t split;                  // MN weights: first k-row taken from r1
   uint32_t split_bytes;           // split * ldb
@@ -201,10 +202,11 @@ template <int W, bool REBASE, int Q0B = 0, int Q0E = loads_per_wave<W>()>
 __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
   constexpr int ROWS = 1024 / (2 * W);
   if constexpr (REBASE) {
-    const uint32_t skip = (uint32_t)kt * BK * op.ldb;
-    const uint64_t base = reinterpret_cast<uint64_t>(op.base) + (live ? skip : 0u);
-    const uint32_t bytes = (live && skip < op.bytes) ? op.bytes - skip : 0u;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const void*>(uni64((int64_t)base)), uni(bytes));
+    // 64-bit window: a group's rows may span more than 4 GiB (ktile.h).
+    const pmx::KTileWindow win = pmx::ktile_window(op.bytes, op.ldb, kt, live);
+    const uint64_t base = reinterpret_cast<uint64_t>(op.base) + win.offset;
+    const __amdgpu_buffer_rsrc_t rk =
+        make_rsrc(reinterpret_cast<const void*>(uni64((int64_t)base)), (uint64_t)uni64((int64_t)win.bytes));
 #pragma unroll
     for (int q0 = Q0B; q0 < Q0E; ++q0) {
       const int q = q0 * NWAVES + wave;
@@ -586,10 +588,10 @@ __device__ __forceinline__ void setup_operands(const GemmParams& P, Tile<KIND, B
     const int64_t rows = ti.row_end - ti.row0;
     tc.A.base = reinterpret_cast<const char*>(P.a.p0 + (int64_t)ti.row0 * P.a.ld);
     tc.A.ldb = (uint32_t)(P.a.ld * 2);
-    tc.A.bytes = (uint32_t)(rows * P.a.ld * 2);
+    tc.A.bytes = (uint64_t)rows * (uint64_t)P.a.ld * 2u;
     tc.B.base = reinterpret_cast<const char*>(P.b.p0 + (int64_t)ti.row0 * P.b.ld);
     tc.B.ldb = (uint32_t)(P.b.ld * 2);
-    tc.B.bytes = (uint32_t)(rows * P.b.ld * 2);
+    tc.B.bytes = (uint64_t)rows * (uint64_t)P.b.ld * 2u;
     mn_offsets<BM, true>(tc.A, wave, lane, (int64_t)ti.mtile * BM, P.M, 0);
     mn_offsets<BN, true>(tc.B, wave, lane, (int64_t)ti.ntile * BN, P.N, 0);
   } else {
@@ -683,7 +685,7 @@ __device__ __forceinline__ TileInfo decode_tile(const GemmParams& P, int64_t til
     ti.mtile = (int32_t)m;
     ti.row0 = P.offsets[g];
     ti.row_end = P.offsets[g + 1];
-    ti.nk = (ti.row_end - ti.row0 + BK - 1) / BK;
+    ti.nk = (int32_t)(((int64_t)ti.row_end - ti.row0 + BK - 1) / BK);
   } else {
     band_order(tile, tpre[G], ntn, m, n);
     // Uniform binary search for the group holding m-tile m.
@@ -759,6 +761,7 @@ __device__ __forceinline__ void block_barrier() {
 template <int KIND, int BM>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P) {
   static_assert(BM == 256, "the schedule below is written for 256 x 256 tiles");
+  static_assert(BK == pmx::kKTileRows, "wgrad K-tile windows are 64 rows deep");
   constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
   constexpr int QA = loads_per_wave<BM>(), QB = loads_per_wave<BN>();  // per wave and K-tile
   __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE_BYTES];
@@ -1104,6 +1107,9 @@ int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int3
                       void* C0, void* C1, int64_t c_copy_stride, int64_t c_split, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || M <= 0 || N <= 0) return PMX_ERR_ARG;
   if (M % 8 || N % 8) return PMX_ERR_SHAPE;
+  // One K-tile (64 rows) of either operand lies within one descriptor; the
+  // group as a whole may span any number of bytes (rebased per K-tile).
+  if (!fits_rsrc(BK, M) || !fits_rsrc(BK, N)) return PMX_ERR_SHAPE;
   if (!A || !B || !offsets || !C0) return PMX_ERR_ARG;
   if (!a16(A) || !a16(B)) return PMX_ERR_SHAPE;
   GemmParams P = {};

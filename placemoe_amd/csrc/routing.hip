@@ -275,9 +275,10 @@ int launch_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32
   const bool lds = C <= kRouteLdsMaxSlots;
   const size_t lds_bytes = lds ? (size_t)C * sizeof(int32_t) : 0;
   if (A == 0) {
-    // No assignments: the table is one zero row; the scan still writes
-    // counts and offsets.
-    fill_i32_kernel<<<(unsigned)((C + 255) / 256), 256, 0, stream>>>(table, C, 0);
+    // No assignments: the table is one zero row and its chunk flag (which
+    // follows it) is clear; the scan still writes counts, offsets and the
+    // status word.
+    fill_i32_kernel<<<(unsigned)((C + 1 + 255) / 256), 256, 0, stream>>>(table, (int64_t)C + 1, 0);
   } else if (lds) {
     route_hist_kernel<true><<<(unsigned)g.nchunks, 64, lds_bytes, stream>>>(
         sel, M, src, src_const, S, E, K, C, A, g.chunk, phys, table, flags);

@@ -17,9 +17,34 @@ combine (``rank_dedup_combine``, veomni/distributed/moe/hiermoe/all_to_all.py:25
 
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import kernels
+
+# Route checks whose status copy has not been looked at yet (forward-only
+# calls have no backward to look at them); each forward polls them without
+# waiting and raises for the first that reports an invalid id.
+_PENDING_CHECKS: list = []
+
+
+def _sync_route_checks() -> bool:
+    """PLACEMOE_AMD_CHECK_ROUTES=1: check every forward's routing on the spot
+    (one stream synchronisation per call)."""
+    return os.environ.get("PLACEMOE_AMD_CHECK_ROUTES", "0") not in ("", "0")
+
+
+def _poll_pending_checks() -> None:
+    keep = []
+    for check in _PENDING_CHECKS:
+        if check.checked:
+            continue
+        if check.ready():
+            check.raise_if_failed()
+        else:
+            keep.append(check)
+    _PENDING_CHECKS[:] = keep[-64:]
 
 
 class _ExpertLayerBase(torch.autograd.Function):
@@ -31,7 +56,27 @@ class _ExpertLayerBase(torch.autograd.Function):
         T, H = hidden.shape
         C, H2, inter = fc2_weight.shape
         assert H2 == H, f"down_proj hidden size {H2} != hidden size {H}"
+        # fc1 must describe the same C copies, hidden size and intermediate size as fc2.
+        assert w_gate.dtype == torch.bfloat16 and w_up.dtype == torch.bfloat16, (
+            f"fc1 weights must be bfloat16, got {w_gate.dtype}/{w_up.dtype}"
+        )
+        assert fc2_weight.dtype == torch.bfloat16, f"fc2 weight must be bfloat16, got {fc2_weight.dtype}"
+        fc1_shape = (C, inter, H) if split else (C, 2 * inter, H)
+        assert tuple(w_gate.shape) == fc1_shape, (
+            f"fc1 weight shape {tuple(w_gate.shape)} does not match fc2 {tuple(fc2_weight.shape)} "
+            f"and hidden size {H} (expected {fc1_shape})"
+        )
+        _poll_pending_checks()
         r = kernels.route(selected, C, mapping=mapping, sources=sources, source=source)
+        # Invalid expert or source ids are clamped on the device and flagged in
+        # the routing status word.  Its copy is checked without a host sync:
+        # at the start of the backward, or by a later forward.
+        check = kernels.RouteCheck(r)
+        if _sync_route_checks():
+            check.raise_if_failed()
+        else:
+            _PENDING_CHECKS.append(check)
+        ctx.route_check = check
         if recorder is not None:
             recorder(r.counts)
         xp = kernels.moe_scatter(hidden, r.pos)
@@ -46,6 +91,7 @@ class _ExpertLayerBase(torch.autograd.Function):
 
     @staticmethod
     def _backward(ctx, grad_out):
+        ctx.route_check.raise_if_failed()
         xp, gu, act, y, pos, offsets, w, w_gate, w_up, fc2_weight = ctx.saved_tensors
         grad_out = grad_out.contiguous()
         need_w, need_x = ctx.needs_input_grad[1], ctx.needs_input_grad[0]

@@ -112,6 +112,35 @@ def route_status(r: Routing) -> int:
     return int(out.value)
 
 
+class RouteCheck:
+    """The routing status word, copied to pinned host memory behind the
+    routing kernels on the same stream.  ``failed()`` waits only for that
+    copy, which the GPU finishes long before the host reaches the backward."""
+
+    def __init__(self, r: Routing):
+        dev = r.workspace.device
+        self._host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        self._host.copy_(r.workspace[:4].view(torch.int32), non_blocking=True)
+        self._event = torch.cuda.Event()
+        self._event.record(torch.cuda.current_stream(dev))
+        self.checked = False
+
+    def ready(self) -> bool:
+        return self._event.query()
+
+    def failed(self) -> bool:
+        self._event.synchronize()
+        return int(self._host[0]) != 0
+
+    def raise_if_failed(self) -> None:
+        self.checked = True
+        if self.failed():
+            raise ValueError(
+                "selected_experts holds an expert id outside [0, num_experts) (or a source id outside the "
+                "mapping's rows); the routing kernels clamped it, so this step's outputs are not valid."
+            )
+
+
 # ---------------------------------------------------------------------------
 # Row movement
 # ---------------------------------------------------------------------------
@@ -213,7 +242,17 @@ def gemm_fc1_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, c
     """(gu [A,2I], act [A,I]) = SwiGLU fc1 over per-copy row groups."""
     dev = _check_dev(x, w_gate, w_up, offsets)
     _bf16("hidden", x)
+    _bf16("fc1 gate weight", w_gate)
+    _bf16("fc1 up weight", w_up)
     A, H = x.shape
+    G, inter, copy_stride = int(num_groups), int(inter), int(copy_stride)
+    assert offsets.dtype == torch.int32 and offsets.numel() == G + 1, "offsets must be int32 [num_groups + 1]"
+    # The kernel reads I*H elements of gate (and of up) rows at g*copy_stride for every group g.
+    need = (G - 1) * copy_stride + inter * H
+    assert copy_stride >= inter * H and w_gate.numel() >= need and w_up.numel() >= need, (
+        f"fc1 weights hold {w_gate.numel()}/{w_up.numel()} elements; {G} copies of [{inter}, {H}] "
+        f"at stride {copy_stride} need {need}"
+    )
     gu = torch.empty((A, 2 * inter), dtype=x.dtype, device=dev)
     act = torch.empty((A, inter), dtype=x.dtype, device=dev)
     _capi.call(
@@ -315,11 +354,20 @@ def group_gemm_tn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, split
 
 
 def replica_fold(grads: torch.Tensor, copy_offsets: torch.Tensor, copy_slots: torch.Tensor, num_experts: int,
-                 slot_tokens: torch.Tensor | None = None, writeback: bool = False) -> torch.Tensor:
-    """fp32 [E, ...] = sum over the active copies of each expert of ``grads`` [C, ...]."""
-    dev = _check_dev(grads, copy_offsets, copy_slots, slot_tokens)
+                 slot_tokens: torch.Tensor | None = None, writeback: bool = False,
+                 status: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [E, ...] = sum over the active copies of each expert of ``grads`` [C, ...].
+
+    A ``copy_slots`` entry outside [0, C) is skipped by the kernel and sets
+    ``status`` (a caller-zeroed int32 device tensor, if given) to 1; nothing
+    here reads it back, so the call never synchronises the host.
+    """
+    dev = _check_dev(grads, copy_offsets, copy_slots, slot_tokens, status)
     _bf16("grads", grads)
     assert copy_offsets.dtype == torch.int32 and copy_slots.dtype == torch.int32
+    assert copy_offsets.numel() == int(num_experts) + 1, "copy_offsets must have num_experts + 1 entries"
+    if status is not None:
+        assert status.dtype == torch.int32 and status.numel() >= 1
     C = grads.shape[0]
     P = grads[0].numel() if C else 0
     out = torch.empty((num_experts,) + tuple(grads.shape[1:]), dtype=torch.float32, device=dev)
@@ -329,6 +377,6 @@ def replica_fold(grads: torch.Tensor, copy_offsets: torch.Tensor, copy_slots: to
     _capi.call(
         "pmx_replica_fold", _ptr(grads), _ptr(copy_offsets), _ptr(copy_slots), _ptr(slot_tokens),
         int(num_experts), C, P, ctypes.cast(out.data_ptr(), ctypes.POINTER(ctypes.c_float)),
-        1 if writeback else 0, _stream(dev),
+        1 if writeback else 0, _ptr(status), _stream(dev),
     )
     return out

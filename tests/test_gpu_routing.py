@@ -88,6 +88,22 @@ def test_route_zero_tokens(cuda):
     r = kernels.route(torch.empty((0, 4), dtype=torch.int64, device=cuda), 6)
     assert r.counts.cpu().tolist() == [0] * 6
     assert r.offsets.cpu().tolist() == [0] * 7
+    assert kernels.route_status(r) == 0
+    # The same through the C ABI with a workspace full of stale bytes: no
+    # assignment means no invalid id, whatever the workspace held before.
+    from placemoe_amd import _capi
+
+    lib = _capi.load()
+    ws_bytes = lib.pmx_route_workspace_bytes(0, 6)
+    ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device=cuda)
+    counts = torch.full((6,), -1, dtype=torch.int32, device=cuda)
+    offsets = torch.full((7,), -1, dtype=torch.int32, device=cuda)
+    stream = torch.cuda.current_stream(cuda).cuda_stream
+    _capi.call("pmx_route", None, None, None, 0, 1, 6, 0, 4, 6, None, counts.data_ptr(), offsets.data_ptr(),
+               None, ws.data_ptr(), ws_bytes, stream)
+    assert counts.cpu().tolist() == [0] * 6 and offsets.cpu().tolist() == [0] * 7
+    assert kernels.route_status(kernels.Routing(phys=None, counts=counts, offsets=offsets, pos=None,
+                                                workspace=ws)) == 0
 
 
 def test_route_out_of_range_is_flagged_not_faulting(cuda):
