@@ -71,6 +71,22 @@ int pmx_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t 
               int32_t* phys, int32_t* counts, int32_t* offsets, int32_t* pos,
               void* workspace, size_t workspace_bytes, pmx_stream_t stream);
 
+/* Allocation-free variant of pmx_route, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It has no counterpart in the reference.  Same kernels and
+ * results as pmx_route; the chunk table lives in a static device array of
+ * 8 MiB per GPU (held until the process ends) instead of a caller workspace,
+ * and the routing status word (0 = every index valid) is written to
+ * `status` (device int32; NULL drops it).  Calls no allocating routine.
+ * Limit: pmx_route_workspace_bytes(T*K, C) must not exceed 8 MiB (every T
+ * when C <= 2000), else PMX_ERR_SHAPE before anything is launched.  Calls
+ * on one GPU share the array: calls that overlap on one GPU (different
+ * streams, or threads) race; calls ordered on one stream do not. */
+int pmx_route_noalloc(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t src_const,
+                      int32_t S, int32_t E, int64_t T, int32_t K, int32_t C,
+                      int32_t* phys, int32_t* counts, int32_t* offsets, int32_t* pos,
+                      int32_t* status, pmx_stream_t stream);
+
 /* Copies the routing status word (0 = all indices valid) to host memory;
  * synchronises `stream`.  For tests and debug validation only. */
 int pmx_route_status(const void* workspace, int32_t* status_host, pmx_stream_t stream);

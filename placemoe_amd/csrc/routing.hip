@@ -14,6 +14,8 @@
 
 #include <string.h>
 
+#include <mutex>
+
 namespace {
 
 constexpr int kRouteLdsMaxSlots = 8192;  // LDS counters up to this many copies
@@ -258,17 +260,19 @@ __global__ __launch_bounds__(64) void route_rank_kernel(const int32_t* __restric
 // positions: T and T*K must fit in 31 bits.
 inline bool rows_fit(int64_t T, int32_t K) { return T <= INT32_MAX / K; }
 
+// `status` receives the routing status word; by default (NULL) it is the
+// first word of the workspace.
 int launch_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t src_const,
                  int32_t S, int32_t E, int64_t A, int32_t K, int32_t C, int32_t* phys,
                  int32_t* counts, int32_t* offsets, int32_t* pos, void* workspace,
-                 size_t workspace_bytes, hipStream_t stream) {
+                 size_t workspace_bytes, hipStream_t stream, int32_t* status = nullptr) {
   if (C <= 0 || C > kRouteMaxSlots || A < 0 || K <= 0) return PMX_ERR_ARG;
   if (A > INT32_MAX) return PMX_ERR_SHAPE;  // positions and counts are int32
   if (!counts || !offsets || !workspace) return PMX_ERR_ARG;
   if (A > 0 && (!sel || !phys || !pos)) return PMX_ERR_ARG;
   if (M != nullptr && (S <= 0 || E <= 0)) return PMX_ERR_ARG;
   if (workspace_bytes < route_ws_bytes(A, C)) return PMX_ERR_ARG;
-  int32_t* status = reinterpret_cast<int32_t*>(workspace);
+  if (status == nullptr) status = reinterpret_cast<int32_t*>(workspace);
   int32_t* table = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + kStatusBytes);
   RouteGeom g = route_geom(A, C);
   int32_t* flags = table + g.nchunks * (int64_t)C;
@@ -565,6 +569,40 @@ int pmx_route_launch(const int64_t* sel, const int64_t* M, const int64_t* src, i
 
 size_t pmx_route_ws_bytes(int64_t A, int32_t C) { return route_ws_bytes(A, C); }
 
+// ---------------------------------------------------------------------------
+// Device scratch of pmx_route_noalloc: the routing chunk table lives in a
+// static device array instead of a caller workspace.  Each GPU holds its own
+// copy until the process ends.  On the host the array's name is only a
+// stand-in, never a device address: host code uses the per-device address
+// that hipGetSymbolAddress returns, taken once per device.
+// ---------------------------------------------------------------------------
+
+constexpr size_t kNoAllocScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up on the first call on
+// that device (with that device current) and kept for later calls.
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return PMX_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return PMX_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PMX_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* pmx_version(void) { return "placemoe_amd 0.1.0 gfx950"; }
@@ -594,6 +632,22 @@ int pmx_route(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t 
   if (T > INT32_MAX / K) return PMX_ERR_SHAPE;
   return launch_route(sel, M, src, src_const, S, E, T * K, K, C, phys, counts, offsets, pos, workspace,
                       workspace_bytes, stream);
+}
+
+int pmx_route_noalloc(const int64_t* sel, const int64_t* M, const int64_t* src, int32_t src_const, int32_t S,
+                      int32_t E, int64_t T, int32_t K, int32_t C, int32_t* phys, int32_t* counts,
+                      int32_t* offsets, int32_t* pos, int32_t* status, pmx_stream_t stream) {
+  if (T < 0 || K <= 0 || C <= 0) return PMX_ERR_ARG;
+  if (M == nullptr && src != nullptr) return PMX_ERR_ARG;
+  if (T > INT32_MAX / K) return PMX_ERR_SHAPE;
+  // The chunk table must fit the static scratch: refuse before any launch.
+  if (route_ws_bytes(T * K, C) > kNoAllocScratchBytes) return PMX_ERR_SHAPE;
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws);
+  if (rc != PMX_OK) return rc;
+  int32_t* st = status != nullptr ? status : static_cast<int32_t*>(ws);
+  return launch_route(sel, M, src, src_const, S, E, T * K, K, C, phys, counts, offsets, pos, ws,
+                      kNoAllocScratchBytes, stream, st);
 }
 
 int pmx_route_status(const void* workspace, int32_t* status_host, pmx_stream_t stream) {
