@@ -117,6 +117,7 @@ struct Operand {
                                   // MN weights: k-rows below / from `split`
   const char* base;               // wgrad operands: the group's first row ...
   uint64_t bytes;                 // ... and the bytes of its rows (descriptor rebased per K-tile)
+  __amdgpu_buffer_rsrc_t rk;      // wgrad operands: descriptor of the K-tile being issued
   uint32_t ldb;                   // bytes between consecutive (k-)rows
   int32_t split;                  // MN weights: first k-row taken from r1
   uint32_t split_bytes;           // split * ldb
@@ -202,15 +203,12 @@ template <int W, bool REBASE, int Q0B = 0, int Q0E = loads_per_wave<W>()>
 __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
   constexpr int ROWS = 1024 / (2 * W);
   if constexpr (REBASE) {
-    // 64-bit window: a group's rows may span more than 4 GiB (ktile.h).
-    const pmx::KTileWindow win = pmx::ktile_window(op.bytes, op.ldb, kt, live);
-    const uint64_t base = reinterpret_cast<uint64_t>(op.base) + win.offset;
-    const __amdgpu_buffer_rsrc_t rk =
-        make_rsrc(reinterpret_cast<const void*>(uni64((int64_t)base)), (uint64_t)uni64((int64_t)win.bytes));
+    // op.rk is the window of the K-tile being issued (rebase_ktile), kept up
+    // to date by the issue cursor.
 #pragma unroll
     for (int q0 = Q0B; q0 < Q0E; ++q0) {
       const int q = q0 * NWAVES + wave;
-      dma16(rk, lds + q * 1024, op.voff[q0], 0u);
+      dma16(op.rk, lds + q * 1024, op.voff[q0], 0u);
     }
   } else {
     const bool tail = kt == op.ktail;
@@ -224,6 +222,15 @@ __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt,
       dma16(!live ? none : second ? op.r1 : op.r0, lds + q * 1024, lane_off(op, q0, tail), soff);
     }
   }
+}
+
+// Point a weight-gradient operand's descriptor at K-tile kt of its group:
+// the window starts at the K-tile's first row and ends with the group, in
+// 64-bit arithmetic (ktile.h).  `live` false: an empty window (loads zeros).
+__device__ __forceinline__ void rebase_ktile(Operand& op, int32_t kt, bool live) {
+  const pmx::KTileWindow win = pmx::ktile_window(op.bytes, op.ldb, kt, live);
+  const uint64_t base = reinterpret_cast<uint64_t>(op.base) + win.offset;
+  op.rk = make_rsrc(reinterpret_cast<const void*>(uni64((int64_t)base)), (uint64_t)uni64((int64_t)win.bytes));
 }
 
 // Issue this wave's share of K-tile kt of a tile into `stage`.  `live` is
@@ -594,6 +601,8 @@ __device__ __forceinline__ void setup_operands(const GemmParams& P, Tile<KIND, B
     tc.B.bytes = (uint64_t)rows * (uint64_t)P.b.ld * 2u;
     mn_offsets<BM, true>(tc.A, wave, lane, (int64_t)ti.mtile * BM, P.M, 0);
     mn_offsets<BN, true>(tc.B, wave, lane, (int64_t)ti.ntile * BN, P.N, 0);
+    rebase_ktile(tc.A, 0, true);
+    rebase_ktile(tc.B, 0, true);
   } else {
     const int64_t rows = ti.row_end - ti.row0 < BM ? ti.row_end - ti.row0 : BM;
     const bf16_t* a0 = P.a.p0 + (int64_t)ti.row0 * P.a.ld;
@@ -672,15 +681,20 @@ __device__ __forceinline__ void band_order(int64_t t, int64_t mtiles, int64_t nt
 
 // The tile list: every kind but TN walks m-tiles of all groups (exclusive
 // prefix `tpre`, ntn n-tiles each); TN walks the tiles_per_group weight tiles
-// of each group, whose K is the group's row count.
+// of each group, whose K is the group's row count.  `local` >= 0 (TN only)
+// names tile `local` of group `tile` instead of a position in the list.
 template <int KIND, int BM>
 __device__ __forceinline__ TileInfo decode_tile(const GemmParams& P, int64_t tile, const int32_t* tpre, int G,
-                                                int64_t ntn, int64_t tiles_per_group) {
+                                                int64_t ntn, int64_t tiles_per_group, int64_t local = -1) {
   TileInfo ti;
   int64_t m, n;
   if constexpr (KIND == KIND_TN) {
-    const int64_t g = tile / tiles_per_group;
-    band_order(tile - g * tiles_per_group, tiles_per_group / ntn, ntn, m, n);
+    int64_t g = tile;
+    if (local < 0) {
+      g = tile / tiles_per_group;
+      local = tile - g * tiles_per_group;
+    }
+    band_order(local, tiles_per_group / ntn, ntn, m, n);
     ti.g = (int32_t)g;
     ti.mtile = (int32_t)m;
     ti.row0 = P.offsets[g];
@@ -741,6 +755,43 @@ __device__ __forceinline__ void block_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Weight-gradient schedule.  A wgrad tile of copy g costs ceil(rows_g / 64)
+// K-tiles, so copies of very different sizes make the round-robin deal of
+// tiles to blocks uneven.  The schedule keeps the deal's structure - the
+// tile list cut into bands of 32 tiles, the 8 m x 4 n tiles that one XCD's
+// 32 blocks multiply side by side sharing operand strips in its L2, and all
+// XCDs working on neighbouring bands at the same time, which lets the
+// XCDs share the K-tile rows in flight through the memory-side cache - and
+// changes two things:
+//   - copies are ordered by K-tile count, largest first, so that a round of
+//     bands costs about the same on every XCD;
+//   - bands are dealt to XCDs in snake order (round r: XCD x takes band
+//     8r + x, or 8r + 7 - x when r is odd), so that the XCD that took the
+//     dearest band of one round takes the cheapest of the next.
+// (A longest-processing-time deal of bands to XCDs balances the work
+// better but lets the XCDs drift apart over different copies' rows; measured
+// slower on every shape.)  Needs a grid of whole XCDs and G <= NTHREADS;
+// otherwise (false) the plain order is used.
+constexpr int kBandTiles = 32;
+constexpr int kNumXcd = 8;
+
+// `order[r]` = the copy of rank r (more K-tiles first, ties by copy index).
+__device__ __noinline__ void build_wgrad_order(const GemmParams& P, int32_t* nk, int32_t* order, int t) {
+  const int G = P.G;
+  if (t < G) nk[t] = (int32_t)(((int64_t)P.offsets[t + 1] - P.offsets[t] + BK - 1) / BK);
+  __syncthreads();
+  if (t < G) {
+    const int32_t mine = nk[t];
+    int32_t rank = 0;
+    for (int g = 0; g < G; ++g) {
+      const int32_t v = nk[g];
+      rank += (v > mine || (v == mine && g < t)) ? 1 : 0;
+    }
+    order[rank] = t;
+  }
+  __syncthreads();
+}
+
 // One block per CU walks its tiles (slot, slot + grid, ...) as one stream of
 // 64-deep K-tiles through two LDS stages: K-tile p of the stream is
 // multiplied from one stage while K-tile p+1 lands in the other.
@@ -758,8 +809,11 @@ __device__ __forceinline__ void block_barrier() {
 // stage just freed before the tile's last k-step is multiplied and the tile
 // is written out (through per-wave epilogue regions outside the stages), so
 // the loads stay in flight across the epilogue.
-template <int KIND, int BM>
+// BAL (weight gradient only): the balanced band order of build_wgrad_order;
+// the host picks it when the grid is 8 XCDs x 32 blocks and G <= NTHREADS.
+template <int KIND, int BM, bool BAL = false>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P) {
+  static_assert(!BAL || KIND == KIND_TN, "the balanced order is the weight gradient's");
   static_assert(BM == 256, "the schedule below is written for 256 x 256 tiles");
   static_assert(BK == pmx::kKTileRows, "wgrad K-tile windows are 64 rows deep");
   constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
@@ -773,12 +827,14 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int G = P.G;
 
+  const int64_t grid = gridDim.x;
   int64_t ntn, tiles_per_group = 0, total;
   if constexpr (KIND == KIND_TN) {
     const int64_t mtn = (P.M + BM - 1) / BM;
     ntn = (P.N + BN - 1) / BN;
     tiles_per_group = mtn * ntn;
     total = tiles_per_group * G;
+    if constexpr (BAL) build_wgrad_order(P, tpre, scan_buf, t);
   } else {
     ntn = (KIND == KIND_FC1) ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
     // Exclusive prefix of m-tiles per group: GPT groups per thread, then a
@@ -815,17 +871,38 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
 
   // XCD-aware order: blocks are dispatched round-robin over the 8 XCDs, so
   // give the blocks of one XCD a contiguous run of each wave of tiles.
-  const int64_t grid = gridDim.x;
   int64_t slot = blockIdx.x;
   if ((grid & 7) == 0) slot = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
+  const int32_t xcd = (int32_t)(blockIdx.x % kNumXcd);
+  const int32_t xj = (int32_t)(blockIdx.x / kNumXcd);  // the block's position in its XCD's bands
+
+  // The block's seq-th output tile; false past its last.  Plain order: tiles
+  // slot, slot + grid, ...  Balanced wgrad order (BAL, grid = 8 XCDs x 32
+  // blocks): copies by rank; in round seq, XCD x takes band
+  // 8 seq + x (8 seq + 7 - x when seq is odd) and its block j tile j of it.
+  auto tile_at = [&](int64_t seq, TileInfo& ti) -> bool {
+    if constexpr (!BAL) {
+      const int64_t tile = slot + seq * grid;
+      if (tile >= total) return false;
+      ti = decode_tile<KIND, BM>(P, tile, tpre, G, ntn, tiles_per_group);
+      return true;
+    } else {
+      const int32_t x = (seq & 1) ? kNumXcd - 1 - xcd : xcd;
+      const int64_t tile = (seq * kNumXcd + x) * kBandTiles + xj;
+      if (tile >= total) return false;
+      const int64_t rank = tile / tiles_per_group;
+      ti = decode_tile<KIND, BM>(P, uni(scan_buf[rank]), tpre, G, ntn, tiles_per_group,
+                                 tile - rank * tiles_per_group);
+      return true;
+    }
+  };
 
   // Consume cursor: the output tile being multiplied.  Tiles without K-tiles
   // (wgrad of an empty group) are written as zeros on the way.
-  int64_t c_tile = slot;
+  int64_t c_seq = 0;
   TileInfo cur;
-  for (;; c_tile += grid) {
-    if (c_tile >= total) return;
-    cur = decode_tile<KIND, BM>(P, c_tile, tpre, G, ntn, tiles_per_group);
+  for (;; ++c_seq) {
+    if (!tile_at(c_seq, cur)) return;
     if (cur.nk > 0) break;
     zero_tile<BM>(P, cur, t);
   }
@@ -833,22 +910,32 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   // Issue cursor: one K-tile in front, over the same tile sequence.  Past the
   // block's last K-tile it issues through an empty descriptor (zeros).
   Tile<KIND, BM> it;
-  int64_t i_tile = c_tile;
+  int64_t i_seq = c_seq;
   int32_t i_kt = 0;
   bool i_live = true;
   it.i = cur;
   setup_operands<KIND, BM>(P, it, wave, lane);
   auto advance_issue = [&]() {
-    if (!i_live || ++i_kt < it.i.nk) return;
+    if (!i_live) return;
+    if (++i_kt < it.i.nk) {
+      if constexpr (KIND == KIND_TN) {
+        rebase_ktile(it.A, i_kt, true);
+        rebase_ktile(it.B, i_kt, true);
+      }
+      return;
+    }
     i_kt = 0;
-    for (i_tile += grid; i_tile < total; i_tile += grid) {
-      it.i = decode_tile<KIND, BM>(P, i_tile, tpre, G, ntn, tiles_per_group);
+    while (tile_at(++i_seq, it.i)) {
       if (it.i.nk > 0) {
         setup_operands<KIND, BM>(P, it, wave, lane);
         return;
       }
     }
     i_live = false;
+    if constexpr (KIND == KIND_TN) {
+      rebase_ktile(it.A, 0, false);
+      rebase_ktile(it.B, 0, false);
+    }
   };
   auto issue_next = [&](char* stage) {
     issue_stage<KIND, BM>(stage, it, i_kt, i_live, wave);
@@ -939,8 +1026,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     // Move the consume cursor on.
     const TileInfo done = cur;
     bool more = false;
-    for (c_tile += grid; c_tile < total; c_tile += grid) {
-      cur = decode_tile<KIND, BM>(P, c_tile, tpre, G, ntn, tiles_per_group);
+    while (tile_at(++c_seq, cur)) {
       if (cur.nk > 0) {
         more = true;
         break;
@@ -984,7 +1070,11 @@ template <int KIND>
 int launch(const GemmParams& P, hipStream_t stream) {
   const int grid = grid_size();
   if (grid <= 0) return PMX_ERR_HIP;
-  grouped_gemm_kernel<KIND, kBM><<<grid, NTHREADS, 0, stream>>>(P);
+  if (KIND == KIND_TN && grid == kNumXcd * kBandTiles && P.G <= NTHREADS) {
+    grouped_gemm_kernel<KIND_TN, kBM, true><<<grid, NTHREADS, 0, stream>>>(P);
+  } else {
+    grouped_gemm_kernel<KIND, kBM><<<grid, NTHREADS, 0, stream>>>(P);
+  }
   PMX_LAUNCH_CHECK();
   return PMX_OK;
 }
