@@ -176,10 +176,22 @@ constexpr int loads_per_wave() { return R * BK * 2 / 1024 / NWAVES; }
 // K-contiguous operand, R rows x 64 k: instruction q = q0*NWAVES + wave
 // covers 8 rows x 128 bytes.  Lane i of instruction q fills row 8q + i/8,
 // physical chunk i%8, i.e. logical chunk (i%8) ^ swz(row).
-// FC1's virtual B rows alternate 32 gate rows (r0) and 32 up rows (r1), so
-// instruction q reads up rows exactly when bit 2 of q is set.
-template <int R, bool SPLIT_ROWS, int Q0B = 0, int Q0E = loads_per_wave<R>()>
+// FC1's virtual B rows alternate 32 gate rows and 32 up rows; a wave's
+// instructions all read one of the two (setup_operands puts it in r0).
+// FAST (K a multiple of 64): no K tail to mask, and `live` is not read: a
+// finished issue cursor keeps its last tile with kt = 0, so its pipeline
+// slots re-load that tile's first K-tile (in bounds; never multiplied).
+template <int R, bool SPLIT_ROWS, int Q0B = 0, int Q0E = loads_per_wave<R>(), bool FAST = false>
 __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
+  if constexpr (FAST) {
+    const uint32_t soff = (uint32_t)kt * (BK * 2);
+#pragma unroll
+    for (int q0 = Q0B; q0 < Q0E; ++q0) {
+      const int q = q0 * NWAVES + wave;
+      dma16(op.r0, lds + q * 1024, op.voff[q0], soff);
+    }
+    return;
+  }
   const uint32_t soff = live ? (uint32_t)kt * (BK * 2) : 0u;
   const bool tail = kt == op.ktail;
   const __amdgpu_buffer_rsrc_t none = empty_rsrc(op.base);
@@ -188,7 +200,7 @@ __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt,
 #pragma unroll
   for (int q0 = Q0B; q0 < Q0E; ++q0) {
     const int q = q0 * NWAVES + wave;
-    dma16((SPLIT_ROWS && ((q >> 2) & 1)) ? r1 : r0, lds + q * 1024, lane_off(op, q0, tail), soff);
+    dma16(r0, lds + q * 1024, lane_off(op, q0, tail), soff);
   }
 }
 
@@ -199,10 +211,19 @@ __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt,
 // with the group, so rows past the group load zeros.  Otherwise (dgrad
 // weights) the K-tile advance is a scalar offset into r0 (k-rows below split)
 // or r1, and the lanes past K are masked in the last K-tile.
-template <int W, bool REBASE, int Q0B = 0, int Q0E = loads_per_wave<W>()>
+// FAST (dgrad weights with K a multiple of 64 and no split): every k-row
+// comes from r0, no K tail, no `live` test (see dma_kc).
+template <int W, bool REBASE, int Q0B = 0, int Q0E = loads_per_wave<W>(), bool FAST = false>
 __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
   constexpr int ROWS = 1024 / (2 * W);
-  if constexpr (REBASE) {
+  if constexpr (FAST && !REBASE) {
+#pragma unroll
+    for (int q0 = Q0B; q0 < Q0E; ++q0) {
+      const int q = q0 * NWAVES + wave;
+      const uint32_t k = (uint32_t)kt * BK + (uint32_t)(q * ROWS);  // first k-row of the instruction
+      dma16(op.r0, lds + q * 1024, op.voff[q0], k * op.ldb);
+    }
+  } else if constexpr (REBASE) {
     // op.rk is the window of the K-tile being issued (rebase_ktile), kept up
     // to date by the issue cursor.
 #pragma unroll
@@ -237,32 +258,33 @@ __device__ __forceinline__ void rebase_ktile(Operand& op, int32_t kt, bool live)
 // false for the pipeline slots past the block's last tile: they go through an
 // empty descriptor, so every step issues the same number of loads.
 // PART selects the operands: 0 = A, 1 = B, 2 = both.
-template <int KIND, int BM, int PART = 2>
+template <int KIND, int BM, bool FAST, int PART = 2>
 __device__ __forceinline__ void issue_stage(char* stage, const Tile<KIND, BM>& tc, int32_t kt, bool live, int wave) {
   char* As = stage;
   char* Bs = stage + BM * BK * 2;
   if constexpr (PART != 1) {
     if constexpr (a_is_mn<KIND>()) dma_mn<BM, true>(As, tc.A, kt, live, wave);
-    else dma_kc<BM, false>(As, tc.A, kt, live, wave);
+    else dma_kc<BM, false, 0, loads_per_wave<BM>(), FAST>(As, tc.A, kt, live, wave);
   }
   if constexpr (PART != 0) {
-    if constexpr (b_is_mn<KIND>()) dma_mn<BN, KIND == KIND_TN>(Bs, tc.B, kt, live, wave);
-    else dma_kc<BN, KIND == KIND_FC1>(Bs, tc.B, kt, live, wave);
+    if constexpr (b_is_mn<KIND>()) dma_mn<BN, KIND == KIND_TN, 0, loads_per_wave<BN>(), FAST>(Bs, tc.B, kt, live, wave);
+    else dma_kc<BN, KIND == KIND_FC1, 0, loads_per_wave<BN>(), FAST>(Bs, tc.B, kt, live, wave);
   }
 }
 
 // Instruction Q0 of this wave's share of operand OPER (0 = A, 1 = B).
-template <int KIND, int BM, int OPER, int Q0>
+template <int KIND, int BM, bool FAST, int OPER, int Q0>
 __device__ __forceinline__ void issue_one(char* stage, const Tile<KIND, BM>& tc, int32_t kt, bool live, int wave) {
   if constexpr (OPER == 0) {
     if constexpr (a_is_mn<KIND>()) dma_mn<BM, true, Q0, Q0 + 1>(stage, tc.A, kt, live, wave);
-    else dma_kc<BM, false, Q0, Q0 + 1>(stage, tc.A, kt, live, wave);
+    else dma_kc<BM, false, Q0, Q0 + 1, FAST>(stage, tc.A, kt, live, wave);
   } else {
     char* Bs = stage + BM * BK * 2;
-    if constexpr (b_is_mn<KIND>()) dma_mn<BN, KIND == KIND_TN, Q0, Q0 + 1>(Bs, tc.B, kt, live, wave);
-    else dma_kc<BN, KIND == KIND_FC1, Q0, Q0 + 1>(Bs, tc.B, kt, live, wave);
+    if constexpr (b_is_mn<KIND>()) dma_mn<BN, KIND == KIND_TN, Q0, Q0 + 1, FAST>(Bs, tc.B, kt, live, wave);
+    else dma_kc<BN, KIND == KIND_FC1, Q0, Q0 + 1, FAST>(Bs, tc.B, kt, live, wave);
   }
 }
+
 
 // Fragment of a K-contiguous tile: lane l holds row (rb + l%32), k = ks*16 + (l/32)*8 + 0..7.
 __device__ __forceinline__ bf16x8_t frag_kc(const char* t, int rb, int ks, int lane) {
@@ -614,9 +636,12 @@ __device__ __forceinline__ void setup_operands(const GemmParams& P, Tile<KIND, B
     const bf16_t* b1 = P.b.p1 + (int64_t)ti.g * P.b.gs1;
     tc.B.base = reinterpret_cast<const char*>(b0);
     if constexpr (KIND == KIND_FC1) {
-      // virtual B rows: per 64 rows, 32 gate rows (r0) then 32 up rows (r1)
-      tc.B.r0 = make_rsrc(b0, (uint64_t)P.I * P.K * 2);
-      tc.B.r1 = make_rsrc(b1, (uint64_t)P.I * P.K * 2);
+      // virtual B rows: per 64 rows, 32 gate rows then 32 up rows.  A wave's
+      // instructions q = q0*NWAVES + wave fill rows 8q .. 8q+7, which are up
+      // rows exactly when bit 2 of the wave index is set, whatever q0: each
+      // wave needs only one of the two descriptors, kept in r0.
+      tc.B.r0 = make_rsrc(((wave >> 2) & 1) ? b1 : b0, (uint64_t)P.I * P.K * 2);
+      tc.B.r1 = tc.B.r0;
       tc.B.ldb = (uint32_t)(P.K * 2);
       int32_t krem;
       k_tail(P.K, tc.B.ktail, krem);
@@ -811,9 +836,14 @@ __device__ __noinline__ void build_wgrad_order(const GemmParams& P, int32_t* nk,
 // the loads stay in flight across the epilogue.
 // BAL (weight gradient only): the balanced band order of build_wgrad_order;
 // the host picks it when the grid is 8 XCDs x 32 blocks and G <= NTHREADS.
-template <int KIND, int BM, bool BAL = false>
+// FAST (ragged-M kinds): K is a multiple of 64 and the dgrad weights are one
+// tensor, so the loads need no K-tail masking, no split test and no `live`
+// test (dma_kc, dma_mn; the slots past the block's last K-tile re-load the
+// first K-tile of its last tile, whose data is never multiplied).
+template <int KIND, int BM, bool BAL = false, bool FAST = false>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P) {
   static_assert(!BAL || KIND == KIND_TN, "the balanced order is the weight gradient's");
+  static_assert(!FAST || KIND != KIND_TN, "the weight gradient has no fast variant");
   static_assert(BM == 256, "the schedule below is written for 256 x 256 tiles");
   static_assert(BK == pmx::kKTileRows, "wgrad K-tile windows are 64 rows deep");
   constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
@@ -938,7 +968,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     }
   };
   auto issue_next = [&](char* stage) {
-    issue_stage<KIND, BM>(stage, it, i_kt, i_live, wave);
+    issue_stage<KIND, BM, FAST>(stage, it, i_kt, i_live, wave);
     advance_issue();
   };
 
@@ -981,8 +1011,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
         static_for<0, QA + QB>([&](auto ll) __attribute__((always_inline)) {
           constexpr int l = decltype(ll)::value;
           if constexpr (SPREAD * l == decltype(ks)::value * NF + j) {
-            if constexpr (l < QA) issue_one<KIND, BM, 0, l>(refill, it, i_kt, i_live, wave);
-            else issue_one<KIND, BM, 1, l - QA>(refill, it, i_kt, i_live, wave);
+            if constexpr (l < QA) issue_one<KIND, BM, FAST, 0, l>(refill, it, i_kt, i_live, wave);
+            else issue_one<KIND, BM, FAST, 1, l - QA>(refill, it, i_kt, i_live, wave);
           }
         });
       }
@@ -1070,10 +1100,19 @@ template <int KIND>
 int launch(const GemmParams& P, hipStream_t stream) {
   const int grid = grid_size();
   if (grid <= 0) return PMX_ERR_HIP;
-  if (KIND == KIND_TN && grid == kNumXcd * kBandTiles && P.G <= NTHREADS) {
-    grouped_gemm_kernel<KIND_TN, kBM, true><<<grid, NTHREADS, 0, stream>>>(P);
+  if constexpr (KIND == KIND_TN) {
+    if (grid == kNumXcd * kBandTiles && P.G <= NTHREADS) {
+      grouped_gemm_kernel<KIND_TN, kBM, true><<<grid, NTHREADS, 0, stream>>>(P);
+    } else {
+      grouped_gemm_kernel<KIND_TN, kBM><<<grid, NTHREADS, 0, stream>>>(P);
+    }
   } else {
-    grouped_gemm_kernel<KIND, kBM><<<grid, NTHREADS, 0, stream>>>(P);
+    // FAST: K a multiple of 64, dgrad weights not split (P.b.split >= K).
+    if (P.K % BK == 0 && (KIND != KIND_NN || P.b.split >= P.K)) {
+      grouped_gemm_kernel<KIND, kBM, false, true><<<grid, NTHREADS, 0, stream>>>(P);
+    } else {
+      grouped_gemm_kernel<KIND, kBM><<<grid, NTHREADS, 0, stream>>>(P);
+    }
   }
   PMX_LAUNCH_CHECK();
   return PMX_OK;
