@@ -110,7 +110,65 @@ def parse():
                    help="first run a plain 1 GiB device copy (reference kernel for HBM-traffic counters)")
     p.add_argument("--vendor-gemm", action="store_true",
                    help="also time the six GEMMs through hipBLASLt, one call per copy, on the same groups")
+    p.add_argument("--layers", type=int, default=1,
+                   help="stack this many layers (own copy weights and placement each) per step; with --config "
+                        "fold, each layer's replica fold runs on a side stream beside the backward of the "
+                        "layers before it; prints the step time only")
     return p.parse_args()
+
+
+def layer_stack(wl, dev, layers: int, steps: int, warmup: int, fold: bool):
+    """`layers` expert layers in a row through the op boundary (each with its
+    own copy weights and registered placement), forward + backward, and with
+    `fold` the replica fold of every layer overlapped with the backward
+    (``OverlappedReplicaSync``).  Returns ms per step."""
+    import placemoe_amd
+    from placemoe_amd.fused_moe import hip_fused_moe_forward
+    from placemoe_amd.placement import PLACEMENTS, LayerPlacement, LayerPlan
+
+    class Experts(torch.nn.Module):
+        def __init__(self, fc1, fc2):
+            super().__init__()
+            self.gate_up_proj = torch.nn.Parameter(fc1)
+            self.down_proj = torch.nn.Parameter(fc2)
+
+    plan = LayerPlan(slot_to_logical=wl.slot_to_logical, source_logical_to_physical=wl.mapping.cpu().numpy(),
+                     owner_slots=wl.owner_slots())
+    mods = {}
+    for i in range(layers):
+        key = f"layers.{i}.mlp.experts"
+        m = Experts(wl.fc1.detach().clone(), wl.fc2.detach().clone())
+        pl = LayerPlacement.from_plan(key, plan, wl.num_experts)
+        pl.token_sources = wl.sources
+        PLACEMENTS.register(pl, m.gate_up_proj, m.down_proj)
+        mods[key] = m
+    sync = placemoe_amd.OverlappedReplicaSync(mods) if fold else None
+    x = wl.hidden.detach().requires_grad_(True)
+    w = wl.routing_weights.detach()
+    dout = torch.randn_like(wl.hidden, dtype=torch.float32).to(torch.bfloat16)
+
+    def step():
+        h = x
+        for key, m in mods.items():
+            m.zero_grad(set_to_none=True)
+            h = hip_fused_moe_forward(wl.num_experts, w, wl.selected, h, None, None, m.down_proj, m.gate_up_proj,
+                                      layer_key=key)
+        h.backward(dout)
+        if sync is not None:
+            sync.finish()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    if sync is not None:
+        sync.remove()
+    PLACEMENTS.clear()
+    return ms
 
 
 def host_cpu() -> dict:
@@ -437,6 +495,14 @@ def main():
     dout = torch.randn((T, H), device=dev, generator=torch.Generator(device=dev).manual_seed(1)).to(torch.bfloat16)
 
     fold = args.config == "fold"
+    if args.layers > 1:
+        ms = layer_stack(wl, dev, args.layers, args.steps, args.warmup, fold)
+        print(json.dumps({"metric": "MoE layer fwd+bwd ms", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+                          "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+                          "config": {"workload": args.config, "layers": args.layers,
+                                     "replica_fold": "overlapped per layer" if fold else None}}), flush=True)
+        return 0
     if fold:
         from placemoe_amd import kernels
         from placemoe_amd.placement import copy_table
@@ -466,12 +532,17 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
+    # Per-kernel durations: the backward's independent GEMM pairs, which the
+    # timed steps run on two streams, are serialized here so that each
+    # kernel's events bracket it alone.
     timer = EventTimer()
+    overlap = experts.set_backward_overlap(False)
     _capi.set_timer(timer)
     for _ in range(args.profile_steps):
         timer.new_step()
         step()
     _capi.set_timer(None)
+    experts.set_backward_overlap(overlap)
     avg = timer.averages()
     kernels_ms = {label: avg.get((name, idx)) for name, idx, label in STAGES if (name, idx) in avg}
     if not kernels_ms:
@@ -519,6 +590,8 @@ def main():
         "permute_gbps": round(permute_gbps, 1),
         "permute_frac_hbm_peak": round(permute_gbps / PEAK_HBM_GBPS, 4),
         "kernel_ms": {k: round(v, 4) for k, v in kernels_ms.items()},
+        "kernel_timing": "HIP events per kernel over --profile-steps extra steps, backward GEMM pairs serialized; "
+                         "the timed steps run fc2 dgrad beside fc2 wgrad and fc1 dgrad beside fc1 wgrad",
         "bandwidth_gbps": bandwidth,
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(dom_tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),

@@ -10,7 +10,7 @@ from .experts import expert_layer  # noqa: F401
 from .fused_moe import apply_veomni_fused_moe_patch, fused_moe_forward, hip_fused_moe_forward  # noqa: F401
 from .kernel_registry import KERNEL_REGISTRY, HardwareRequirement, KernelSpec  # noqa: F401
 from .placement import PLACEMENTS, LayerPlacement, LayerPlan, PlaceMoETopology, mirrored_r2_plan  # noqa: F401
-from .replica import fold_replica_gradients, sync_redundant_gradients  # noqa: F401
+from .replica import OverlappedReplicaSync, fold_replica_gradients, sync_redundant_gradients  # noqa: F401
 from .statistics import ProfileStatistics, RouteStatisticsRecorder, profile_route_statistics  # noqa: F401
 
 __version__ = "0.1.0"

@@ -35,6 +35,30 @@ def _sync_route_checks() -> bool:
     return os.environ.get("PLACEMOE_AMD_CHECK_ROUTES", "0") not in ("", "0")
 
 
+# Backward GEMM pairs that do not depend on each other (fc2 dgrad and fc2
+# wgrad; fc1 dgrad and fc1 wgrad) run on two streams, so that the tail of
+# one persistent GEMM (its last, partly filled round of tiles) runs beside
+# the other's blocks.  Streams keep the default priority.
+_OVERLAP = True
+_SIDE_STREAMS: dict = {}
+
+
+def set_backward_overlap(enabled: bool) -> bool:
+    """Run the backward's independent GEMM pairs on two streams (default) or
+    all on the caller's stream; returns the previous setting."""
+    global _OVERLAP
+    prev, _OVERLAP = _OVERLAP, bool(enabled)
+    return prev
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    s = _SIDE_STREAMS.get(device)
+    if s is None:
+        s = torch.cuda.Stream(device=device)
+        _SIDE_STREAMS[device] = s
+    return s
+
+
 def _poll_pending_checks() -> None:
     keep = []
     for check in _PENDING_CHECKS:
@@ -96,16 +120,32 @@ class _ExpertLayerBase(torch.autograd.Function):
         grad_out = grad_out.contiguous()
         need_w, need_x = ctx.needs_input_grad[1], ctx.needs_input_grad[0]
         dy, dw = kernels.combine_bwd(grad_out, y, pos, w)
+        main = torch.cuda.current_stream(dy.device)
+        side = _side_stream(dy.device) if _OVERLAP else main
+        # The weight gradients go to the side stream, each after the main
+        # stream has produced its inputs; the dgrads stay on the main stream.
+        d_fc2 = d_fc1 = None
+        if ctx.fc2_needs_grad:
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                d_fc2 = kernels.group_gemm_tn(dy, act, offsets)
         dg1 = kernels.gemm_fc2_dgrad_swiglu(dy, fc2_weight, gu, offsets)
-        d_fc2 = kernels.group_gemm_tn(dy, act, offsets) if ctx.fc2_needs_grad else None
-        d_fc1 = None
         if ctx.fc1_needs_grad:
-            d_fc1 = kernels.group_gemm_tn(dg1, xp, offsets, split=ctx.inter if ctx.split else None)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                d_fc1 = kernels.group_gemm_tn(dg1, xp, offsets, split=ctx.inter if ctx.split else None)
         dx = None
         if need_x:
             # Merged weights: w_gate is the whole [C, 2I, H] gate_up_proj.
             dxp = kernels.group_gemm_nn(dg1, w_gate, offsets, b_second=w_up if ctx.split else None)
             dx = kernels.moe_gather(dxp, pos)
+        if side is not main:
+            # The caller's stream waits for the weight gradients, which were
+            # allocated on the side stream and are used on the caller's.
+            main.wait_stream(side)
+            for t in (d_fc2, *(d_fc1 if isinstance(d_fc1, tuple) else (d_fc1,))):
+                if t is not None:
+                    t.record_stream(main)
         return dx, (dw if need_w else None), d_fc1, d_fc2
 
 

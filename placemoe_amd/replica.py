@@ -64,6 +64,95 @@ def sync_redundant_gradients(modules: dict[str, torch.nn.Module]) -> dict[str, t
     return out
 
 
+class OverlappedReplicaSync:
+    """The fold of ``sync_redundant_gradients``, layer by layer, overlapped
+    with the rest of the backward.
+
+    As soon as both expert gradients of a registered layer have been
+    accumulated (a post-accumulate-grad hook on ``gate_up_proj`` and
+    ``down_proj``), that layer's fold is enqueued on a side stream that
+    waits for the caller's stream at that point; the backward of the layers
+    before it goes on on the caller's stream meanwhile.  The reference does
+    the same per layer on a separate stream ordered by ready events
+    (veomni/distributed/moe/hiermoe/expert_swap.py:5259-5262, :5318-5336).
+    ``finish()`` makes the caller's stream wait for every fold and returns the
+    fp32 logical gradients per layer, as ``sync_redundant_gradients`` does.
+
+    One fold per backward while ``enabled``; with gradient accumulation,
+    disable it for all but the last micro-batch.  The side stream keeps the
+    default priority.
+    """
+
+    def __init__(self, modules: dict[str, torch.nn.Module], *, writeback: bool = True):
+        self.enabled = True
+        self._modules = dict(modules)
+        self._writeback = writeback
+        self._arrived: dict[str, set] = {}
+        self._results: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
+        self._streams: dict[torch.device, torch.cuda.Stream] = {}
+        self._handles = []
+        for key, module in self._modules.items():
+            for param in (module.gate_up_proj, module.down_proj):
+                self._handles.append(param.register_post_accumulate_grad_hook(self._hook(key)))
+
+    def _hook(self, key: str):
+        def on_grad(param: torch.Tensor) -> None:
+            if not self.enabled:
+                return
+            arrived = self._arrived.setdefault(key, set())
+            arrived.add(id(param))
+            if len(arrived) == 2:
+                arrived.clear()
+                self._enqueue(key)
+
+        return on_grad
+
+    def _stream(self, device: torch.device) -> torch.cuda.Stream:
+        s = self._streams.get(device)
+        if s is None:
+            s = torch.cuda.Stream(device=device)
+            self._streams[device] = s
+        return s
+
+    @torch.no_grad()
+    def _enqueue(self, key: str) -> None:
+        placement = PLACEMENTS.get(key)
+        if placement is None:
+            return
+        module = self._modules[key]
+        grads = (module.gate_up_proj.grad, module.down_proj.grad)
+        device = grads[0].device
+        main = torch.cuda.current_stream(device)
+        side = self._stream(device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            folded = tuple(fold_replica_gradients(placement, g, writeback=self._writeback) for g in grads)
+        for g in grads:
+            g.record_stream(side)
+        self._results[key] = folded
+
+    def finish(self) -> dict[str, tuple[torch.Tensor, torch.Tensor]]:
+        """The caller's stream waits for every enqueued fold; returns the fp32
+        logical gradients of the layers folded since the last call and clears
+        their accumulated token counts."""
+        for device, side in self._streams.items():
+            main = torch.cuda.current_stream(device)
+            main.wait_stream(side)
+        out, self._results = self._results, {}
+        for key, folded in out.items():
+            for t in folded:
+                t.record_stream(torch.cuda.current_stream(t.device))
+            placement = PLACEMENTS.get(key)
+            if placement is not None:
+                placement.clear_slot_tokens()
+        return out
+
+    def remove(self) -> None:
+        for h in self._handles:
+            h.remove()
+        self._handles = []
+
+
 # ---------------------------------------------------------------------------
 # Cross-rank replica-gradient exchange: one rank's side
 # ---------------------------------------------------------------------------
