@@ -36,15 +36,16 @@ import torch
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 
-# HBM bytes per launch of a workload's dominant kernel, measured in separate
-# rocprofv3 runs of this benchmark (FETCH_SIZE, then WRITE_SIZE, each scaled by
-# what the counter reads for a 1 GiB device copy: x2.00 and x1.00).  Counters
-# cannot be read from inside a timed run, so the figure is carried here.
+# HBM bytes per launch of the candidate dominant kernels of the default
+# workload, measured on this build in separate rocprofv3 runs of this
+# benchmark (FETCH_SIZE, then WRITE_SIZE, each scaled by what the counter reads
+# for a 1 GiB device copy: x2.00 and x1.00; profiles/hbm_traffic_dsv3.md).
+# Counters cannot be read from inside a timed run, so the figure is carried
+# here; other workloads report traffic null.
 MEASURED_TRAFFIC_BYTES = {
-    ("qwen3", "fc1_fwd"): (2437 + 576) * 2**20,
-    ("qwen3", "fc1_wgrad"): (1687 + 960) * 2**20,
-    ("dsv3", "fc1_fwd"): (6315 + 769) * 2**20,
-    ("dsv3", "fc1_dgrad"): (6415 + 896) * 2**20,
+    ("dsv3", "fc1_fwd"): (6700 + 768) * 2**20,
+    ("dsv3", "fc1_wgrad"): (5401 + 896) * 2**20,
+    ("dsv3", "fc1_dgrad"): (7151 + 896) * 2**20,
 }
 
 # Entry-point call order inside one step; repeated names are told apart by
@@ -250,6 +251,27 @@ def cpu_baseline(wl, sample_tokens: int | None, backward: bool):
                f"{host['affinity']} in this process's affinity set)")
     return {"value": value, "unit": "ms", "cores": threads, "kind": "port", "sample": sample,
             "cpu_model": host["model"], "host_cpu_count": host["cpu_count"], "affinity_cpus": host["affinity"]}
+
+
+def dense_gemm_tflops(dev, n: int = 8192, reps: int = 10) -> float:
+    """bf16 TFLOP/s of the vendor library (hipBLASLt through torch.matmul) on
+    one dense n x n x n product of random data: the measured MFMA reference
+    beside the 2.5 PFLOP/s spec (random operands keep the part at its power
+    limit, as the layer's GEMMs do)."""
+    g = torch.Generator(device=dev).manual_seed(9)
+    a = torch.randn((n, n), generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn((n, n), generator=g, device=dev).to(torch.bfloat16)
+    c = torch.matmul(a, b)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        torch.matmul(a, b, out=c)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    del a, b, c
+    return round(2 * n**3 / (ms * 1e-3) / 1e12, 1)
 
 
 def device_copy_gbps(dev, reps: int = 10) -> float:
@@ -603,6 +625,8 @@ def main():
     result["aux_bandwidth_gbps"] = aux_bw
     result["aux_config"] = aux_cfg
     result["device_copy_gbps"] = device_copy_gbps(dev)
+    result["dense_vendor_gemm_tflops"] = dense_gemm_tflops(dev)
+    result["roofline"]["frac_of_dense_vendor_gemm"] = round(dom_tflops / result["dense_vendor_gemm_tflops"], 4)
     if args.vendor_gemm:
         result["vendor_gemm"] = vendor_gemms(wl, dev)
     if not args.no_cpu_baseline:
