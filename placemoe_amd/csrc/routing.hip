@@ -521,6 +521,57 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* 
   }
 }
 
+// Top-1 combine gradient with one wave per token: dY[pos[t]] = bf16(dout[t] * w[t])
+// and dw[t] = bf16(sum_h fp32(bf16(dout[t,h] * Y[pos[t],h]))), the sum kept in
+// lane partials and reduced across the wave (no LDS, no block barrier).  Each
+// lane moves UNR 16-byte chunks of both rows per pass, all loads first.
+template <int UNR>
+__global__ __launch_bounds__(256) void combine_bwd_top1_kernel(const bf16_t* __restrict__ dout,
+                                                               const bf16_t* __restrict__ Y,
+                                                               const int32_t* __restrict__ pos,
+                                                               const bf16_t* __restrict__ w, int64_t T, int64_t H,
+                                                               bf16_t* __restrict__ dY, bf16_t* __restrict__ dw) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const int64_t row = (int64_t)pos[t] * H;
+  const float wk = bf16_to_f32(w[t]);
+  const int64_t n8 = H / 8;
+  const uint4* d_row = reinterpret_cast<const uint4*>(dout + t * H);
+  const uint4* y_row = reinterpret_cast<const uint4*>(Y + row);
+  uint4* g_row = reinterpret_cast<uint4*>(dY + row);
+  float part = 0.f;
+  for (int64_t base = lane; base < n8; base += 64 * UNR) {
+    uint4 dv[UNR], yv[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t i = base + 64 * u;
+      if (i < n8) {
+        dv[u] = ld_stream(d_row + i);
+        yv[u] = ld_stream(y_row + i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int64_t i = base + 64 * u;
+      if (i < n8) {
+        float d[8], y[8], g[8];
+        unpack8(dv[u], d);
+        unpack8(yv[u], y);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) g[j] = d[j] * wk;
+        st_stream(g_row + i, pack8(g));
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += round_bf16(d[j] * y[j]);
+        part += s;
+      }
+    }
+  }
+  part = wave_sum(part);
+  if (lane == 0) dw[t] = (bf16_t)f32_to_bf16(part);
+}
+
 // order[pos[i]] = i : the inverse of the stable scatter index.
 __global__ void invert_kernel(const int32_t* __restrict__ pos, int64_t N, int32_t* __restrict__ order) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -727,6 +778,15 @@ int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const v
   if (T == 0) return PMX_OK;
   if (!dout || !Y || !pos || !w || !dY || !dw) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
+  if (K == 1 && H % 8 == 0 && H >= 2048 && aligned16(dout) && aligned16(Y) && aligned16(dY)) {
+    // top-1 rows of at least 2048 columns: a wave per token (4 tokens per block)
+    const int64_t blocks = (T + 3) / 4;
+    if (blocks > 0x7fffffff) return PMX_ERR_SHAPE;
+    combine_bwd_top1_kernel<7><<<(unsigned)blocks, 256, 0, stream>>>(
+        (const bf16_t*)dout, (const bf16_t*)Y, pos, (const bf16_t*)w, T, H, (bf16_t*)dY, (bf16_t*)dw);
+    PMX_LAUNCH_CHECK();
+    return PMX_OK;
+  }
   if (H % 8 == 0 && aligned16(dout) && aligned16(Y) && aligned16(dY)) {
 #define PMX_COMBINE_BWD(KC)                                                                            \
   combine_bwd_kernel<true, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos, \
