@@ -37,15 +37,19 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 
 # HBM bytes per launch of the candidate dominant kernels of the default
-# workload, measured on this build in separate rocprofv3 runs of this
-# benchmark (FETCH_SIZE, then WRITE_SIZE, each scaled by what the counter reads
-# for a 1 GiB device copy: x2.00 and x1.00; profiles/hbm_traffic_dsv3.md).
-# Counters cannot be read from inside a timed run, so the figure is carried
-# here; other workloads report traffic null.
+# workload and of the Qwen3-shape workload, measured on this build in separate
+# rocprofv3 runs of this benchmark (FETCH_SIZE, then WRITE_SIZE, each scaled by
+# what the counter reads for a 1 GiB device copy: x2.00 and x1.00;
+# profiles/hbm_traffic_dsv3.md, profiles/hbm_traffic_qwen3.md).  Counters
+# cannot be read from inside a timed run, so the figure is carried here; other
+# workloads report traffic null.
 MEASURED_TRAFFIC_BYTES = {
-    ("dsv3", "fc1_fwd"): (6700 + 768) * 2**20,
-    ("dsv3", "fc1_wgrad"): (5401 + 896) * 2**20,
-    ("dsv3", "fc1_dgrad"): (7151 + 896) * 2**20,
+    ("dsv3", "fc1_fwd"): (6990 + 877) * 2**20,
+    ("dsv3", "fc1_wgrad"): (5416 + 896) * 2**20,
+    ("dsv3", "fc1_dgrad"): (6825 + 896) * 2**20,
+    ("qwen3", "fc1_fwd"): (2433 + 654) * 2**20,
+    ("qwen3", "fc1_wgrad"): (1338 + 960) * 2**20,
+    ("qwen3", "fc1_dgrad"): (2098 + 512) * 2**20,
 }
 
 # Entry-point call order inside one step; repeated names are told apart by
