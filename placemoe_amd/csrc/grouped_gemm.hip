@@ -788,23 +788,31 @@ __device__ __forceinline__ void block_barrier() {
 // tiles to blocks uneven.  The schedule keeps the deal's structure - the
 // tile list cut into bands of 32 tiles, the 8 m x 4 n tiles that one XCD's
 // 32 blocks multiply side by side sharing operand strips in its L2, and all
-// XCDs working on neighbouring bands at the same time, which lets the
-// XCDs share the K-tile rows in flight through the memory-side cache - and
-// changes two things:
-//   - copies are ordered by K-tile count, largest first, so that a round of
-//     bands costs about the same on every XCD;
-//   - bands are dealt to XCDs in snake order (round r: XCD x takes band
-//     8r + x, or 8r + 7 - x when r is odd), so that the XCD that took the
-//     dearest band of one round takes the cheapest of the next.
-// (A longest-processing-time deal of bands to XCDs balances the work
-// better but lets the XCDs drift apart over different copies' rows; measured
-// slower on every shape.)  Needs a grid of whole XCDs and G <= NTHREADS;
-// otherwise (false) the plain order is used.
+// XCDs working on the 8 neighbouring bands of one round at the same time,
+// which lets the XCDs share the K-tile rows in flight through the
+// memory-side cache - and changes two things:
+//   - copies are ordered by K-tile count, largest first, so that the bands
+//     of a round cost about the same and fall in cost within the round;
+//   - within each round the XCD with the most K-tiles dealt so far takes the
+//     cheapest band, the next one the next cheapest, and so on (the deal is
+//     worked out once per block, before its first tile).
+// (A longest-processing-time deal of bands to XCDs across rounds balances
+// the work as well but lets the XCDs drift apart over different copies'
+// rows; measured slower on every shape.  Alternating the direction of the
+// deal from round to round keeps the rounds but balances less: on the
+// DeepSeek-V3-shape share 96% against 98% of the mean per block.)  Needs a
+// grid of whole XCDs and G <= NTHREADS; otherwise (false) the plain order
+// is used.  Rounds past what the LDS holds alternate direction.
 constexpr int kBandTiles = 32;
 constexpr int kNumXcd = 8;
 
-// `order[r]` = the copy of rank r (more K-tiles first, ties by copy index).
-__device__ __noinline__ void build_wgrad_order(const GemmParams& P, int32_t* nk, int32_t* order, int t) {
+// `order[r]` = the copy of rank r (more K-tiles first, ties by copy index);
+// `deal[r]` (bytes after nk[G]) = the band of round r, 0..7 within the round,
+// that XCD `xcd` takes, for the first `cap` rounds (the return value).
+// `costs` is scratch of `cost_slots` int32 (LDS not yet in use).
+__device__ __noinline__ int32_t build_wgrad_order(const GemmParams& P, int32_t* nk, int32_t* order, int t,
+                                                  int64_t total, int64_t tiles_per_group, int32_t xcd,
+                                                  int32_t* costs, int32_t cost_slots) {
   const int G = P.G;
   if (t < G) nk[t] = (int32_t)(((int64_t)P.offsets[t + 1] - P.offsets[t] + BK - 1) / BK);
   __syncthreads();
@@ -818,6 +826,37 @@ __device__ __noinline__ void build_wgrad_order(const GemmParams& P, int32_t* nk,
     order[rank] = t;
   }
   __syncthreads();
+  // Cost of every band: the K-tiles of its first tile's copy (the dearest of
+  // the band: copies come largest first); 0 past the last tile.
+  const int64_t bands = (total + kBandTiles - 1) / kBandTiles;
+  const int64_t rounds = (bands + kNumXcd - 1) / kNumXcd;
+  int64_t cap = (int64_t)(kMaxGroups + 1 - G) * 4;
+  if (cap > cost_slots / kNumXcd) cap = cost_slots / kNumXcd;
+  if (cap > rounds) cap = rounds;
+  for (int64_t b = t; b < cap * kNumXcd; b += NTHREADS) {
+    const int64_t tile = b * kBandTiles;
+    costs[b] = tile < total ? nk[order[tile / tiles_per_group]] : 0;
+  }
+  __syncthreads();
+  if (t < 64) {
+    // Lanes 0..7 stand for the XCDs; `cum` = K-tiles dealt to XCD `t`.
+    unsigned char* deal = reinterpret_cast<unsigned char*>(nk + G);
+    int32_t cum = 0;
+    for (int32_t r = 0; r < (int32_t)cap; ++r) {
+      const int32_t cost = t < kNumXcd ? costs[r * kNumXcd + t] : 0;
+      int32_t rank = 0;  // XCDs with more K-tiles so far (ties: lower index)
+#pragma unroll
+      for (int y = 0; y < kNumXcd; ++y) {
+        const int32_t cy = __builtin_amdgcn_readlane(cum, y);
+        rank += (cy > cum || (cy == cum && y < t)) ? 1 : 0;
+      }
+      const int32_t band = rank < kNumXcd ? kNumXcd - 1 - rank : 0;
+      cum += __shfl(cost, band);
+      if (t == xcd) deal[r] = (unsigned char)band;
+    }
+  }
+  __syncthreads();
+  return (int32_t)cap;
 }
 
 // One block per CU walks its tiles (slot, slot + grid, ...) as one stream of
@@ -861,13 +900,19 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   const int G = P.G;
 
   const int64_t grid = gridDim.x;
+  const int32_t xcd = (int32_t)(blockIdx.x % kNumXcd);
+  const int32_t xj = (int32_t)(blockIdx.x / kNumXcd);  // the block's position in its XCD's bands
   int64_t ntn, tiles_per_group = 0, total;
+  int32_t deal_rounds = 0;  // BAL: rounds whose band comes from the deal table
   if constexpr (KIND == KIND_TN) {
     const int64_t mtn = (P.M + BM - 1) / BM;
     ntn = (P.N + BN - 1) / BN;
     tiles_per_group = mtn * ntn;
     total = tiles_per_group * G;
-    if constexpr (BAL) build_wgrad_order(P, tpre, scan_buf, t);
+    if constexpr (BAL) {
+      deal_rounds = uni(build_wgrad_order(P, tpre, scan_buf, t, total, tiles_per_group, xcd,
+                                          reinterpret_cast<int32_t*>(lds), (int32_t)(sizeof(lds) / sizeof(int32_t))));
+    }
   } else {
     ntn = (KIND == KIND_FC1) ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
     // Exclusive prefix of m-tiles per group: GPT groups per thread, then a
@@ -906,13 +951,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   // give the blocks of one XCD a contiguous run of each wave of tiles.
   int64_t slot = blockIdx.x;
   if ((grid & 7) == 0) slot = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
-  const int32_t xcd = (int32_t)(blockIdx.x % kNumXcd);
-  const int32_t xj = (int32_t)(blockIdx.x / kNumXcd);  // the block's position in its XCD's bands
 
   // The block's seq-th output tile; false past its last.  Plain order: tiles
   // slot, slot + grid, ...  Balanced wgrad order (BAL, grid = 8 XCDs x 32
-  // blocks): copies by rank; in round seq, XCD x takes band
-  // 8 seq + x (8 seq + 7 - x when seq is odd) and its block j tile j of it.
+  // blocks): copies by rank; in round seq, this block's XCD takes band
+  // 8 seq + deal[seq] (past the table: 8 seq + x, or 8 seq + 7 - x when seq
+  // is odd) and its block j tile j of it.
+  const unsigned char* deal = reinterpret_cast<const unsigned char*>(tpre + G);
   auto tile_at = [&](int64_t seq, TileInfo& ti) -> bool {
     if constexpr (!BAL) {
       const int64_t tile = slot + seq * grid;
@@ -920,7 +965,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       ti = decode_tile<KIND, BM>(P, tile, tpre, G, ntn, tiles_per_group);
       return true;
     } else {
-      const int32_t x = (seq & 1) ? kNumXcd - 1 - xcd : xcd;
+      const int32_t x = seq < deal_rounds ? uni((int32_t)deal[seq]) : ((seq & 1) ? kNumXcd - 1 - xcd : xcd);
       const int64_t tile = (seq * kNumXcd + x) * kBandTiles + xj;
       if (tile >= total) return false;
       const int64_t rank = tile / tiles_per_group;
