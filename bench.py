@@ -57,14 +57,17 @@ MEASURED_TRAFFIC_BYTES = {
 STAGES = [
     ("pmx_route", 0, "route"),
     ("pmx_moe_scatter", 0, "permute"),
+    ("pmx_moe_scatter_src", 0, "permute"),
     ("pmx_gemm_fc1_swiglu_fwd", 0, "fc1_fwd"),
     ("pmx_group_gemm_nt", 0, "fc2_fwd"),
+    ("pmx_group_gemm_nt_combine_top1", 0, "fc2_fwd"),
     ("pmx_combine_fwd", 0, "combine_fwd"),
     ("pmx_combine_bwd", 0, "combine_bwd"),
     ("pmx_gemm_fc2_dgrad_swiglu_bwd", 0, "fc2_dgrad"),
     ("pmx_group_gemm_tn", 0, "fc2_wgrad"),
     ("pmx_group_gemm_tn", 1, "fc1_wgrad"),
     ("pmx_group_gemm_nn", 0, "fc1_dgrad"),
+    ("pmx_group_gemm_nn_unpermute_top1", 0, "fc1_dgrad"),
     ("pmx_moe_gather", 0, "unpermute_grad"),
     ("pmx_replica_fold", 0, "fold_gate_up"),
     ("pmx_replica_fold", 1, "fold_down"),
@@ -115,6 +118,9 @@ def parse():
                    help="first run a plain 1 GiB device copy (reference kernel for HBM-traffic counters)")
     p.add_argument("--vendor-gemm", action="store_true",
                    help="also time the six GEMMs through hipBLASLt, one call per copy, on the same groups")
+    p.add_argument("--no-top1-fusion", action="store_true",
+                   help="top-1 workloads: run the combine and the unpermute gradient as separate kernels "
+                        "instead of in the fc2 and fc1-dgrad epilogues")
     p.add_argument("--layers", type=int, default=1,
                    help="stack this many layers (own copy weights and placement each) per step; with --config "
                         "fold, each layer's replica fold runs on a side stream beside the backward of the "
@@ -500,6 +506,8 @@ def main():
     from placemoe_amd import _capi, experts
     from placemoe_amd.workloads import algorithmic_work, make_workload
 
+    if args.no_top1_fusion:
+        experts.set_top1_fusion(False)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.calibrate_copy:
@@ -593,6 +601,13 @@ def main():
         for label, per_copy in (("fold_gate_up", 2 * I * H), ("fold_down", H * I)):
             bw[label] = C * per_copy * 2 + wl.num_experts * per_copy * 4 + C * per_copy * 2
     bandwidth = {k: round(v / (kernels_ms[k] * 1e-3) / 1e9, 1) for k, v in bw.items() if k in kernels_ms}
+    # Top-1 layers run the combine in fc2's epilogue and the unpermute gradient
+    # in the fc1 dgrad's: those two kernels' times are inside the GEMMs'.
+    fused = {}
+    if ("pmx_group_gemm_nt_combine_top1", 0) in avg:
+        fused["fc2_fwd"] = "combine_fwd"
+    if ("pmx_group_gemm_nn_unpermute_top1", 0) in avg:
+        fused["fc1_dgrad"] = "unpermute_grad"
 
     result = {
         "metric": "MoE layer fwd+bwd ms; grouped-GEMM TFLOP/s (%MFMA peak); permute GB/s",
@@ -619,6 +634,7 @@ def main():
         "kernel_timing": "HIP events per kernel over --profile-steps extra steps, backward GEMM pairs serialized; "
                          "the timed steps run fc2 dgrad beside fc2 wgrad and fc1 dgrad beside fc1 wgrad",
         "bandwidth_gbps": bandwidth,
+        "fused": fused,
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(dom_tflops, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(dom_tflops / PEAK_BF16_TFLOPS, 4),
                      "traffic": MEASURED_TRAFFIC_BYTES.get((args.config, dominant))},

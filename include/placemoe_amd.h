@@ -100,6 +100,18 @@ int pmx_route_status(const void* workspace, int32_t* status_host, pmx_stream_t s
 int pmx_moe_scatter(const void* X, const int32_t* pos, int64_t T, int32_t K, int64_t H,
                     void* Xp, pmx_stream_t stream);
 
+/* pmx_moe_scatter that also records where each row came from:
+ * row_src[pos[t,k]] = t*K + k (int32 [T*K]; NULL: not written) and, given
+ * the router weights w (bf16 [T,K]), each row's weight row_w[pos[t,k]] =
+ * w[t,k] (bf16 [T*K]; w and row_w both given or both NULL, and only with
+ * row_src).  With top-1 routing (K = 1) row_src[r] is the token of row r:
+ * the row map of pmx_group_gemm_nt_combine_top1 and
+ * pmx_group_gemm_nn_unpermute_top1.  Replaces moe_scatter (moe.py:299-333)
+ * plus the inverse of the scatter index that moe_gather's backward reads
+ * (moe.py:126-159). */
+int pmx_moe_scatter_src(const void* X, const int32_t* pos, const void* w, int64_t T, int32_t K,
+                        int64_t H, void* Xp, int32_t* row_src, void* row_w, pmx_stream_t stream);
+
 /* out[t] = bf16( sum_k fp32(Y[pos[t,k]]) ).  Y [T*K,H] bf16 -> out [T,H] bf16.
  * Replaces moe_gather (veomni/ops/kernels/moe/_kernels/kernel/moe.py:126-159). */
 int pmx_moe_gather(const void* Y, const int32_t* pos, int64_t T, int32_t K, int64_t H,
@@ -162,6 +174,21 @@ int pmx_gemm_fc1_swiglu_fwd(const void* X, const void* w_gate, const void* w_up,
 int pmx_group_gemm_nt(const void* A, const void* B, const int32_t* offsets, int32_t G,
                       int64_t M, int64_t N, int64_t K, void* C, pmx_stream_t stream);
 
+/* Top-1 routing only (K = 1: every token has exactly one row): pmx_group_gemm_nt
+ * with the router-weighted combine in its epilogue.  Writes C [M,N] as
+ * pmx_group_gemm_nt does and out[row_token[r]] = bf16(0 + bf16(C[r] * row_weight[r]))
+ * (out [M,N], row_weight bf16 [M]: the router weight of row r), bit-identical
+ * to pmx_combine_fwd(C, pos, w, M, 1, N, out) when row_token and row_weight
+ * are the row map of pos and w (pmx_moe_scatter_src).  Rows whose row_token
+ * lies outside [0, M) are not combined.  row_token, row_weight and out are all
+ * given or all NULL (NULL: pmx_group_gemm_nt).  Replaces
+ * group_gemm_same_nk(transpose_b=True) (group_gemm.py:170-247) followed by
+ * rank_dedup_combine (all_to_all.py:2539-2564) for a top-1 layer. */
+int pmx_group_gemm_nt_combine_top1(const void* A, const void* B, const int32_t* offsets,
+                                   int32_t G, int64_t M, int64_t N, int64_t K, void* C,
+                                   const int32_t* row_token, const void* row_weight, void* out,
+                                   pmx_stream_t stream);
+
 /* Ragged-M grouped GEMM, B not transposed: C[a] = bf16(A[a] @ B[g]), B [G,K,N];
  * B rows k >= b_split come from B1 (for split fc1 weights), else from B0;
  * pass B1 = NULL for a single tensor.  dgrad fc1 (A = dG1 [A,2I]).
@@ -169,6 +196,19 @@ int pmx_group_gemm_nt(const void* A, const void* B, const int32_t* offsets, int3
 int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_copy_stride,
                       int64_t b_split, const int32_t* offsets, int32_t G, int64_t M,
                       int64_t N, int64_t K, void* C, pmx_stream_t stream);
+
+/* Top-1 routing only: pmx_group_gemm_nn whose output row r is written to row
+ * row_token[r] of C [M,N] (NULL: row r, as pmx_group_gemm_nn).  With row_token
+ * the inverse of pos this is the unpermute gradient of a top-1 layer,
+ * bit-identical to pmx_group_gemm_nn followed by pmx_moe_gather(.., K = 1, ..).
+ * Rows whose row_token lies outside [0, M) are not written.  Replaces
+ * group_gemm_same_nk(transpose_b=False) (group_gemm.py:170-247) followed by
+ * moe_gather (moe.py:126-159) for a top-1 layer. */
+int pmx_group_gemm_nn_unpermute_top1(const void* A, const void* B0, const void* B1,
+                                     int64_t b_copy_stride, int64_t b_split,
+                                     const int32_t* offsets, int32_t G, int64_t M, int64_t N,
+                                     int64_t K, const int32_t* row_token, void* C,
+                                     pmx_stream_t stream);
 
 /* dgrad fc2 followed by the SwiGLU backward:
  *   dact = bf16(dY[a] @ down[g])                      ([A,I])

@@ -41,6 +41,10 @@ SIGNATURES = {
     ),
     "pmx_route_status": (c_int, [c_void_p, _i32p, c_void_p]),
     "pmx_moe_scatter": (c_int, [c_void_p, c_void_p, c_int64, c_int32, c_int64, c_void_p, c_void_p]),
+    "pmx_moe_scatter_src": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
     "pmx_moe_gather": (c_int, [c_void_p, c_void_p, c_int64, c_int32, c_int64, c_void_p, c_void_p]),
     "pmx_combine_fwd": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int64, c_void_p, c_void_p]),
     "pmx_combine_bwd": (
@@ -61,10 +65,20 @@ SIGNATURES = {
         c_int,
         [c_void_p, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p],
     ),
+    "pmx_group_gemm_nt_combine_top1": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p],
+    ),
     "pmx_group_gemm_nn": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64,
          c_void_p, c_void_p],
+    ),
+    "pmx_group_gemm_nn_unpermute_top1": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int32, c_int64, c_int64, c_int64,
+         c_void_p, c_void_p, c_void_p],
     ),
     "pmx_gemm_fc2_dgrad_swiglu_bwd": (
         c_int,

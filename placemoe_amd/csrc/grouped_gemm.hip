@@ -87,6 +87,12 @@ struct GemmParams {
   bf16_t* gu;  // written by KIND_FC1
   bf16_t* act;
   const bf16_t* gin;  // KIND_NNS: the forward's gate/up rows [A, 2I]
+  // Top-1 row map (KIND_NN, KIND_NT; null: none).  KIND_NN writes output row
+  // r to row row_tok[r] of c0 instead of row r.  KIND_NT writes row r to c0
+  // and also cout[row_tok[r]] = bf16(0 + bf16(row * row_w[r])).
+  const int32_t* row_tok;
+  const bf16_t* row_w;
+  bf16_t* cout;
 };
 
 template <int KIND>
@@ -473,6 +479,24 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
   // per-lane address arithmetic stays here instead of being hoisted out of
   // the tile loop, where it would hold registers through every K step.
   asm volatile("" : "+v"(lane));
+  // Top-1 row map (KIND_NT, KIND_NN): both rounds' row targets (and, for the
+  // combine, the rows' router weights) are loaded before the first store.
+  // One counter tracks this wave's loads and stores in issue order, so a load
+  // issued after the first round's stores would wait for them as well.
+  // Targets outside [0, M) are not written.
+  const bool mapped = (KIND == KIND_NT || KIND == KIND_NN) && P.row_tok != nullptr;
+  int32_t dst[16];
+  float wt[16];
+  if constexpr (KIND == KIND_NT || KIND == KIND_NN) {
+    if (mapped) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int64_t row = ti.row0 + wm * WROWS + (q >> 3) * 64 + (q & 7) * 8 + (lane >> 3);
+        dst[q] = row < ti.row_end ? P.row_tok[row] : -1;
+        if constexpr (KIND == KIND_NT) wt[q] = row < ti.row_end ? bf16_to_f32(P.row_w[row]) : 0.f;
+      }
+    }
+  }
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     const int64_t rb = wm * WROWS + half * 64;  // first tile row of the round
@@ -538,7 +562,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
           st_stream(P.c0 + row * 2 * I + I + j, pack8(du));
         }
       }
-    } else {
+    } else if constexpr (KIND == KIND_TN) {
       stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
       const int cc = lane & 7;  // 16-byte chunk (8 columns) of the wave's 64
       const int64_t col = (int64_t)ti.ntile * BN + wn * WCOLS + cc * 8;
@@ -546,15 +570,36 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
       for (int q = 0; q < 8; ++q) {
         const int rl = q * 8 + (lane >> 3);
         const uint4 v = staged_chunk(stage, wave, rl, cc);
-        if constexpr (KIND == KIND_TN) {
-          const int64_t m = (int64_t)ti.mtile * BM + rb + rl;
-          if (m < P.M && col < P.N) {
-            bf16_t* crow = m < P.csplit ? P.c0 + ti.g * P.cgs + m * P.ldc : P.c1 + ti.g * P.cgs + (m - P.csplit) * P.ldc;
-            st_stream(crow + col, v);
+        const int64_t m = (int64_t)ti.mtile * BM + rb + rl;
+        if (m < P.M && col < P.N) {
+          bf16_t* crow = m < P.csplit ? P.c0 + ti.g * P.cgs + m * P.ldc : P.c1 + ti.g * P.cgs + (m - P.csplit) * P.ldc;
+          st_stream(crow + col, v);
+        }
+      }
+    } else {
+      const int cc = lane & 7;  // 16-byte chunk (8 columns) of the wave's 64
+      const int64_t col = (int64_t)ti.ntile * BN + wn * WCOLS + cc * 8;
+      stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int rl = q * 8 + (lane >> 3);
+        const uint4 v = staged_chunk(stage, wave, rl, cc);
+        const int64_t row = ti.row0 + rb + rl;
+        if (row < ti.row_end && col < P.N) {
+          const int32_t d = dst[half * 8 + q];
+          if (KIND == KIND_NN && mapped) {
+            if ((uint32_t)d < (uint32_t)P.M) st_stream(P.c0 + (int64_t)d * P.ldc + col, v);
+          } else {
+            st_stream(P.c0 + row * P.ldc + col, v);
           }
-        } else {
-          const int64_t row = ti.row0 + rb + rl;
-          if (row < ti.row_end && col < P.N) st_stream(P.c0 + row * P.ldc + col, v);
+          if (KIND == KIND_NT && mapped && (uint32_t)d < (uint32_t)P.M) {
+            // the weighted combine of a top-1 row, as the combine kernel rounds it
+            float f[8];
+            unpack8(v, f);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = 0.f + round_bf16(f[j] * wt[half * 8 + q]);
+            st_stream(P.cout + (int64_t)d * P.ldc + col, pack8(f));
+          }
         }
       }
     }
@@ -1212,32 +1257,54 @@ int pmx_gemm_fc1_swiglu_fwd(const void* X, const void* w_gate, const void* w_up,
 
 int pmx_group_gemm_nt(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
                       int64_t K, void* C, pmx_stream_t stream) {
+  return pmx_group_gemm_nt_combine_top1(A, B, offsets, G, M, N, K, C, nullptr, nullptr, nullptr, stream);
+}
+
+int pmx_group_gemm_nt_combine_top1(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M,
+                                   int64_t N, int64_t K, void* C, const int32_t* row_token,
+                                   const void* row_weight, void* out, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || M < 0 || N <= 0 || K <= 0) return PMX_ERR_ARG;
   if (N % 8 || K % 8 || M > INT32_MAX) return PMX_ERR_SHAPE;  // row offsets are int32
   if (M == 0) return PMX_OK;
   if (!A || !B || !offsets || !C) return PMX_ERR_ARG;
-  if (!a16(A) || !a16(B)) return PMX_ERR_SHAPE;
+  if (!a16(A) || !a16(B) || !a16(C)) return PMX_ERR_SHAPE;
+  // the combine needs all three of its arguments, or none
+  if ((row_token != nullptr) != (out != nullptr) || (row_token != nullptr) != (row_weight != nullptr)) {
+    return PMX_ERR_ARG;
+  }
+  if (out && !a16(out)) return PMX_ERR_SHAPE;
   if (!fits_rsrc(N, K) || !fits_rsrc(kBM, K)) return PMX_ERR_SHAPE;
   GemmParams P = {};
   P.a = one(A, 0, K);
   P.b = one(B, N * K, K);
   P.offsets = offsets;
   P.G = G;
+  P.M = M;
   P.N = N;
   P.K = K;
   P.c0 = static_cast<bf16_t*>(C);
   P.ldc = N;
+  P.row_tok = row_token;
+  P.row_w = static_cast<const bf16_t*>(row_weight);
+  P.cout = static_cast<bf16_t*>(out);
   return launch<KIND_NT>(P, stream);
 }
 
 int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_copy_stride, int64_t b_split,
                       const int32_t* offsets, int32_t G, int64_t M, int64_t N, int64_t K, void* C,
                       pmx_stream_t stream) {
+  return pmx_group_gemm_nn_unpermute_top1(A, B0, B1, b_copy_stride, b_split, offsets, G, M, N, K, nullptr, C,
+                                          stream);
+}
+
+int pmx_group_gemm_nn_unpermute_top1(const void* A, const void* B0, const void* B1, int64_t b_copy_stride,
+                                     int64_t b_split, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
+                                     int64_t K, const int32_t* row_token, void* C, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || M < 0 || N <= 0 || K <= 0) return PMX_ERR_ARG;
   if (N % 8 || K % 8 || M > INT32_MAX) return PMX_ERR_SHAPE;  // row offsets are int32
   if (M == 0) return PMX_OK;
   if (!A || !B0 || !offsets || !C) return PMX_ERR_ARG;
-  if (!a16(A) || !a16(B0) || (B1 && !a16(B1))) return PMX_ERR_SHAPE;
+  if (!a16(A) || !a16(B0) || (B1 && !a16(B1)) || !a16(C)) return PMX_ERR_SHAPE;
   if (!fits_rsrc(K, N) || !fits_rsrc(kBM, K)) return PMX_ERR_SHAPE;
   GemmParams P = {};
   P.a = one(A, 0, K);
@@ -1250,10 +1317,12 @@ int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_c
   }
   P.offsets = offsets;
   P.G = G;
+  P.M = M;
   P.N = N;
   P.K = K;
   P.c0 = static_cast<bf16_t*>(C);
   P.ldc = N;
+  P.row_tok = row_token;
   return launch<KIND_NN>(P, stream);
 }
 

@@ -340,9 +340,18 @@ inline unsigned row_threads(int64_t H) {
 template <bool VEC, bool STREAM_ST = false>
 __global__ __launch_bounds__(kRowThreads) void scatter_rows_kernel(const bf16_t* __restrict__ X,
                                                            const int32_t* __restrict__ pos, int32_t K,
-                                                           int64_t H, bf16_t* __restrict__ Xp) {
+                                                           int64_t H, bf16_t* __restrict__ Xp,
+                                                           int32_t* __restrict__ row_src,
+                                                           const bf16_t* __restrict__ w,
+                                                           bf16_t* __restrict__ row_w) {
   const int64_t t = blockIdx.x;
   const int32_t* p = pos + t * K;
+  if (row_src != nullptr) {
+    for (int32_t k = threadIdx.x; k < K; k += blockDim.x) {
+      row_src[p[k]] = (int32_t)(t * K + k);
+      if (row_w != nullptr) row_w[p[k]] = w[t * K + k];
+    }
+  }
   if (VEC) {
     const int64_t n8 = H / 8;
     const uint4* src = reinterpret_cast<const uint4*>(X + t * H);
@@ -713,19 +722,30 @@ int pmx_route_status(const void* workspace, int32_t* status_host, pmx_stream_t s
 
 int pmx_moe_scatter(const void* X, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* Xp,
                     pmx_stream_t stream) {
+  return pmx_moe_scatter_src(X, pos, nullptr, T, K, H, Xp, nullptr, nullptr, stream);
+}
+
+int pmx_moe_scatter_src(const void* X, const int32_t* pos, const void* w, int64_t T, int32_t K, int64_t H,
+                        void* Xp, int32_t* row_src, void* row_w, pmx_stream_t stream) {
   if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
   if (!rows_fit(T, K)) return PMX_ERR_SHAPE;
-  if (T == 0 || H == 0) return PMX_OK;
+  if ((w != nullptr) != (row_w != nullptr) || (row_w != nullptr && row_src == nullptr)) return PMX_ERR_ARG;
+  if (T == 0 || (H == 0 && row_src == nullptr)) return PMX_OK;
   if (!X || !pos || !Xp) return PMX_ERR_ARG;
   const unsigned th = row_threads(H);
+  const bf16_t* wb = static_cast<const bf16_t*>(w);
+  bf16_t* rw = static_cast<bf16_t*>(row_w);
   if (H % 8 == 0 && aligned16(X) && aligned16(Xp)) {
     if (K == 1) {
-      scatter_rows_kernel<true, true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp);
+      scatter_rows_kernel<true, true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp,
+                                                                      row_src, wb, rw);
     } else {
-      scatter_rows_kernel<true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp);
+      scatter_rows_kernel<true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp, row_src,
+                                                                wb, rw);
     }
   } else {
-    scatter_rows_kernel<false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp);
+    scatter_rows_kernel<false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, pos, K, H, (bf16_t*)Xp, row_src,
+                                                               wb, rw);
   }
   PMX_LAUNCH_CHECK();
   return PMX_OK;

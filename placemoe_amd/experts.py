@@ -4,6 +4,8 @@ Forward:  route (M table -> histogram -> scan -> stable scatter index) ->
 permute -> fc1 + SwiGLU -> fc2 -> router-weighted combine.
 Backward: combine gradient -> fc2 dgrad + SwiGLU backward -> fc2 wgrad ->
 fc1 dgrad -> fc1 wgrad -> unpermute gradient.
+With top-1 routing the combine runs in fc2's epilogue and the unpermute
+gradient in the fc1 dgrad's (bit-identical; ``set_top1_fusion``).
 
 Every step is a gfx950 kernel of ``libplacemoe_amd.so``; no step has a torch
 or CPU fallback.  The composition follows the reference's EP + PlaceMoE
@@ -48,6 +50,23 @@ def set_backward_overlap(enabled: bool) -> bool:
     all on the caller's stream; returns the previous setting."""
     global _OVERLAP
     prev, _OVERLAP = _OVERLAP, bool(enabled)
+    return prev
+
+
+# Top-1 layers (every token routed to one copy) fold two row kernels into
+# GEMM epilogues: the router-weighted combine into fc2 (which then writes the
+# layer output beside Y) and the unpermute gradient into the fc1 dgrad (which
+# writes each row straight to its token).  Results are bit-identical to the
+# separate kernels.
+_TOP1_FUSION = True
+
+
+def set_top1_fusion(enabled: bool) -> bool:
+    """Fold the combine and the unpermute gradient of top-1 layers into the
+    fc2 and fc1-dgrad GEMMs (default) or run them as separate kernels;
+    returns the previous setting."""
+    global _TOP1_FUSION
+    prev, _TOP1_FUSION = _TOP1_FUSION, bool(enabled)
     return prev
 
 
@@ -103,11 +122,18 @@ class _ExpertLayerBase(torch.autograd.Function):
         ctx.route_check = check
         if recorder is not None:
             recorder(r.counts)
-        xp = kernels.moe_scatter(hidden, r.pos)
+        row_src = None
+        if r.pos.shape[1] == 1 and _TOP1_FUSION:
+            xp, row_src, row_w = kernels.moe_scatter_src(hidden, r.pos, routing_weights)
+        else:
+            xp = kernels.moe_scatter(hidden, r.pos)
         gu, act = kernels.gemm_fc1_swiglu(xp, w_gate, w_up, copy_stride, r.offsets, C, inter)
-        y = kernels.group_gemm_nt(act, fc2_weight, r.offsets)
-        out = kernels.combine_fwd(y, r.pos, routing_weights)
-        ctx.save_for_backward(xp, gu, act, y, r.pos, r.offsets, routing_weights, w_gate, w_up, fc2_weight)
+        if row_src is not None:
+            y, out = kernels.group_gemm_nt_combine_top1(act, fc2_weight, r.offsets, row_src, row_w)
+        else:
+            y = kernels.group_gemm_nt(act, fc2_weight, r.offsets)
+            out = kernels.combine_fwd(y, r.pos, routing_weights)
+        ctx.save_for_backward(xp, gu, act, y, r.pos, r.offsets, routing_weights, w_gate, w_up, fc2_weight, row_src)
         ctx.split = split
         ctx.inter = inter
         ctx.routing = r
@@ -116,7 +142,7 @@ class _ExpertLayerBase(torch.autograd.Function):
     @staticmethod
     def _backward(ctx, grad_out):
         ctx.route_check.raise_if_failed()
-        xp, gu, act, y, pos, offsets, w, w_gate, w_up, fc2_weight = ctx.saved_tensors
+        xp, gu, act, y, pos, offsets, w, w_gate, w_up, fc2_weight, row_src = ctx.saved_tensors
         grad_out = grad_out.contiguous()
         need_w, need_x = ctx.needs_input_grad[1], ctx.needs_input_grad[0]
         dy, dw = kernels.combine_bwd(grad_out, y, pos, w)
@@ -137,8 +163,12 @@ class _ExpertLayerBase(torch.autograd.Function):
         dx = None
         if need_x:
             # Merged weights: w_gate is the whole [C, 2I, H] gate_up_proj.
-            dxp = kernels.group_gemm_nn(dg1, w_gate, offsets, b_second=w_up if ctx.split else None)
-            dx = kernels.moe_gather(dxp, pos)
+            b_second = w_up if ctx.split else None
+            if row_src is not None:
+                dx = kernels.group_gemm_nn_unpermute_top1(dg1, w_gate, offsets, row_src, b_second=b_second)
+            else:
+                dxp = kernels.group_gemm_nn(dg1, w_gate, offsets, b_second=b_second)
+                dx = kernels.moe_gather(dxp, pos)
         if side is not main:
             # The caller's stream waits for the weight gradients, which were
             # allocated on the side stream and are used on the caller's.

@@ -158,6 +158,27 @@ def moe_scatter(x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def moe_scatter_src(x: torch.Tensor, pos: torch.Tensor, w: torch.Tensor | None = None):
+    """moe_scatter that also returns each row's source: row_src[pos[t,k]] =
+    t*K + k (int32 [T*K]), and with the router weights ``w`` [T, K] each row's
+    weight row_w[pos[t,k]] = w[t,k] -> (Xp, row_src, row_w or None)."""
+    dev = _check_dev(x, pos, w)
+    _bf16("x", x)
+    assert pos.dtype == torch.int32 and pos.is_contiguous()
+    T, H = x.shape
+    K = pos.shape[1]
+    out = torch.empty((T * K, H), dtype=x.dtype, device=dev)
+    src = torch.empty(T * K, dtype=torch.int32, device=dev)
+    row_w = None
+    if w is not None:
+        _bf16("routing weights", w)
+        assert w.numel() == T * K, "routing weights: one per (token, k)"
+        row_w = torch.empty(T * K, dtype=w.dtype, device=dev)
+    _capi.call("pmx_moe_scatter_src", _ptr(x), _ptr(pos), _ptr(w), T, K, H, _ptr(out), _ptr(src), _ptr(row_w),
+               _stream(dev))
+    return out, src, row_w
+
+
 def moe_gather(y: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
     """out[t] = bf16(sum_k fp32(y[pos[t,k]]))  ->  [T, H]."""
     dev = _check_dev(y, pos)
@@ -276,10 +297,40 @@ def group_gemm_nt(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor) -> to
     return c
 
 
+def group_gemm_nt_combine_top1(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, row_token: torch.Tensor,
+                               row_weight: torch.Tensor):
+    """Top-1 layers: C = group_gemm_nt(a, b, offsets) and, in the same kernel,
+    out[row_token[r]] = bf16(C[r] * row_weight[r]) (the combine) -> (C, out)."""
+    dev = _check_dev(a, b, offsets, row_token, row_weight)
+    _bf16("a", a)
+    _bf16("b", b)
+    _bf16("row weights", row_weight)
+    G, N, K = b.shape
+    M = a.shape[0]
+    assert a.shape[1] == K, "a and b disagree on K"
+    assert offsets.numel() == G + 1
+    assert row_token.dtype == torch.int32 and row_token.is_contiguous() and row_token.numel() == M
+    assert row_weight.numel() == M, "top-1 routing weights: one per row"
+    c = torch.empty((M, N), dtype=a.dtype, device=dev)
+    out = torch.empty((M, N), dtype=a.dtype, device=dev)
+    _capi.call("pmx_group_gemm_nt_combine_top1", _ptr(a), _ptr(b), _ptr(offsets), G, M, N, K, _ptr(c),
+               _ptr(row_token), _ptr(row_weight), _ptr(out), _stream(dev))
+    return c, out
+
+
+def group_gemm_nn_unpermute_top1(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, row_token: torch.Tensor,
+                                 b_second: torch.Tensor | None = None) -> torch.Tensor:
+    """Top-1 layers: group_gemm_nn whose row r is written to row row_token[r]
+    (the unpermute gradient in the same kernel)."""
+    assert row_token.dtype == torch.int32 and row_token.is_contiguous() and row_token.numel() == a.shape[0]
+    return group_gemm_nn(a, b, offsets, b_second=b_second, row_token=row_token)
+
+
 def group_gemm_nn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor,
-                  b_second: torch.Tensor | None = None) -> torch.Tensor:
-    """C[rows of g] = a[rows of g] @ cat(b, b_second, dim=1)[g], b: [G, K(, +K2), N]."""
-    dev = _check_dev(a, b, offsets, b_second)
+                  b_second: torch.Tensor | None = None, row_token: torch.Tensor | None = None) -> torch.Tensor:
+    """C[rows of g] = a[rows of g] @ cat(b, b_second, dim=1)[g], b: [G, K(, +K2), N];
+    with ``row_token`` (top-1 layers) row r goes to row row_token[r] of C."""
+    dev = _check_dev(a, b, offsets, b_second, row_token)
     _bf16("a", a)
     _bf16("b", b)
     G, K0, N = b.shape
@@ -291,10 +342,13 @@ def group_gemm_nn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor,
     assert offsets.numel() == G + 1
     M = a.shape[0]
     c = torch.empty((M, N), dtype=a.dtype, device=dev)
-    _capi.call(
-        "pmx_group_gemm_nn", _ptr(a), _ptr(b), _ptr(b_second), K0 * N, K0 if b_second is not None else 0,
-        _ptr(offsets), G, M, N, K, _ptr(c), _stream(dev),
-    )
+    split = K0 if b_second is not None else 0
+    if row_token is None:
+        _capi.call("pmx_group_gemm_nn", _ptr(a), _ptr(b), _ptr(b_second), K0 * N, split, _ptr(offsets), G, M, N, K,
+                   _ptr(c), _stream(dev))
+    else:
+        _capi.call("pmx_group_gemm_nn_unpermute_top1", _ptr(a), _ptr(b), _ptr(b_second), K0 * N, split,
+                   _ptr(offsets), G, M, N, K, _ptr(row_token), _ptr(c), _stream(dev))
     return c
 
 
