@@ -121,6 +121,8 @@ def parse():
     p.add_argument("--no-top1-fusion", action="store_true",
                    help="top-1 workloads: run the combine and the unpermute gradient as separate kernels "
                         "instead of in the fc2 and fc1-dgrad epilogues")
+    p.add_argument("--no-backward-overlap", action="store_true",
+                   help="run the backward's independent GEMM pairs one after the other on one stream")
     p.add_argument("--layers", type=int, default=1,
                    help="stack this many layers (own copy weights and placement each) per step; with --config "
                         "fold, each layer's replica fold runs on a side stream beside the backward of the "
@@ -508,6 +510,9 @@ def main():
 
     if args.no_top1_fusion:
         experts.set_top1_fusion(False)
+    if args.no_backward_overlap:
+        experts.set_backward_overlap(False)
+
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.calibrate_copy:
@@ -567,8 +572,9 @@ def main():
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
 
     # Per-kernel durations: the backward's independent GEMM pairs, which the
-    # timed steps run on two streams, are serialized here so that each
+    # timed steps may run on two streams, are serialized here so that each
     # kernel's events bracket it alone.
+    timed_overlap = experts.uses_backward_overlap(T * K, H, I)
     timer = EventTimer()
     overlap = experts.set_backward_overlap(False)
     _capi.set_timer(timer)
@@ -631,8 +637,8 @@ def main():
         "permute_gbps": round(permute_gbps, 1),
         "permute_frac_hbm_peak": round(permute_gbps / PEAK_HBM_GBPS, 4),
         "kernel_ms": {k: round(v, 4) for k, v in kernels_ms.items()},
-        "kernel_timing": "HIP events per kernel over --profile-steps extra steps, backward GEMM pairs serialized; "
-                         "the timed steps run fc2 dgrad beside fc2 wgrad and fc1 dgrad beside fc1 wgrad",
+        "kernel_timing": "HIP events per kernel over --profile-steps extra steps, backward GEMM pairs serialized",
+        "backward_streams": 2 if timed_overlap else 1,
         "bandwidth_gbps": bandwidth,
         "fused": fused,
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(dom_tflops, 1),

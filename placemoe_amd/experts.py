@@ -38,19 +38,35 @@ def _sync_route_checks() -> bool:
 
 
 # Backward GEMM pairs that do not depend on each other (fc2 dgrad and fc2
-# wgrad; fc1 dgrad and fc1 wgrad) run on two streams, so that the tail of
+# wgrad; fc1 dgrad and fc1 wgrad) can run on two streams, so that the tail of
 # one persistent GEMM (its last, partly filled round of tiles) runs beside
-# the other's blocks.  Streams keep the default priority.
-_OVERLAP = True
+# the other's blocks.  That pays off for short GEMMs and costs for long ones,
+# whose weight gradient deals its tiles to blocks assuming they all start
+# together (measured, layer fwd+bwd: Qwen3-30B-A3B shape, A*H*I = 2.1e11,
+# 4.80 -> 4.73 ms and with the replica fold 6.57 -> 6.49 ms; DeepSeek-V3
+# shape, 9.6e11, 15.70 -> 16.26 ms; skewed 96-copy shape, 8.3e11, 15.33 ->
+# 15.62 ms).  By default (None) the two streams are used when
+# rows * H * I < _OVERLAP_MAX_WORK.  Streams keep the default priority.
+_OVERLAP = None
+_OVERLAP_MAX_WORK = 4e11
 _SIDE_STREAMS: dict = {}
 
 
-def set_backward_overlap(enabled: bool) -> bool:
-    """Run the backward's independent GEMM pairs on two streams (default) or
-    all on the caller's stream; returns the previous setting."""
+def set_backward_overlap(enabled: bool | None) -> bool | None:
+    """Run the backward's independent GEMM pairs on two streams (True), all
+    on the caller's stream (False), or choose by GEMM size (None, the
+    default); returns the previous setting."""
     global _OVERLAP
-    prev, _OVERLAP = _OVERLAP, bool(enabled)
+    prev, _OVERLAP = _OVERLAP, (None if enabled is None else bool(enabled))
     return prev
+
+
+def uses_backward_overlap(rows: int, hidden: int, inter: int) -> bool:
+    """Whether the backward of a layer with `rows` received rows, hidden size
+    and intermediate size runs its independent GEMM pairs on two streams."""
+    if _OVERLAP is not None:
+        return _OVERLAP
+    return rows * hidden * inter < _OVERLAP_MAX_WORK
 
 
 # Top-1 layers (every token routed to one copy) fold two row kernels into
@@ -147,7 +163,7 @@ class _ExpertLayerBase(torch.autograd.Function):
         need_w, need_x = ctx.needs_input_grad[1], ctx.needs_input_grad[0]
         dy, dw = kernels.combine_bwd(grad_out, y, pos, w)
         main = torch.cuda.current_stream(dy.device)
-        side = _side_stream(dy.device) if _OVERLAP else main
+        side = _side_stream(dy.device) if uses_backward_overlap(dy.shape[0], dy.shape[1], ctx.inter) else main
         # The weight gradients go to the side stream, each after the main
         # stream has produced its inputs; the dgrads stay on the main stream.
         d_fc2 = d_fc1 = None

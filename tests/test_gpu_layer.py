@@ -223,3 +223,29 @@ def test_layer_with_no_tokens(cuda):
     out.backward(torch.zeros_like(out))
     assert x.grad.shape == (0, H) and w.grad.shape == (0, wl.K)
     assert torch.count_nonzero(fc1.grad).item() == 0 and torch.count_nonzero(fc2.grad).item() == 0
+
+
+@pytest.mark.parametrize("name,tokens,slots", [("qwen3", 512, None), ("dsv3", 1024, 4)])
+def test_backward_on_one_or_two_streams_is_bitwise_identical(cuda, name, tokens, slots):
+    wl = make_workload(name, tokens=tokens, num_slots=slots)
+    print(f"backward streams {name}: T={wl.T} K={wl.K} C={wl.C}", flush=True)
+    dout = torch.randn((wl.T, wl.H), generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(cuda)
+    src = None if wl.sources is None else wl.sources.to(cuda)
+    results = []
+    prev = experts.set_backward_overlap(None)
+    try:
+        for overlap in (True, False):
+            experts.set_backward_overlap(overlap)
+            x = wl.hidden.to(cuda).requires_grad_(True)
+            w = wl.routing_weights.to(cuda).requires_grad_(True)
+            fc1 = wl.fc1.to(cuda).requires_grad_(True)
+            fc2 = wl.fc2.to(cuda).requires_grad_(True)
+            out = experts.expert_layer(x, w, wl.selected.to(cuda), fc2, fc1_1_2_weight=fc1,
+                                       mapping=wl.mapping.to(cuda), sources=src)
+            out.backward(dout)
+            torch.cuda.synchronize()
+            results.append([t.clone() for t in (x.grad, w.grad, fc1.grad, fc2.grad)])
+    finally:
+        experts.set_backward_overlap(prev)
+    for a, b, n in zip(results[0], results[1], ("d_hidden", "d_weights", "d_gate_up", "d_down")):
+        assert_exact(a, b, f"{n}: two streams vs one")

@@ -57,3 +57,23 @@ def test_algorithmic_work_formulas():
     w = algorithmic_work(T=16384, K=8, H=2048, I=768, C=160)
     assert w["gemm_fwd_flops"] + w["gemm_bwd_flops"] == 18 * 131072 * 2048 * 768
     assert abs(w["permute_bytes"] / 1e9 - 0.605) < 1e-3
+
+
+def test_backward_overlap_follows_gemm_size():
+    """The two-stream backward is chosen for the short-GEMM shapes (Qwen3,
+    fold) and not for the long ones (DeepSeek-V3 share, skew), unless set."""
+    from placemoe_amd import experts
+
+    prev = experts.set_backward_overlap(None)
+    try:
+        sizes = {}
+        for name in ("qwen3", "fold", "dsv3", "skew"):
+            wl = make_workload(name, weights=False)
+            sizes[name] = experts.uses_backward_overlap(wl.T * wl.K, wl.H, wl.I)
+        assert sizes == {"qwen3": True, "fold": True, "dsv3": False, "skew": False}
+        experts.set_backward_overlap(True)
+        assert experts.uses_backward_overlap(65536, 7168, 2048)
+        experts.set_backward_overlap(False)
+        assert not experts.uses_backward_overlap(1024, 2048, 768)
+    finally:
+        experts.set_backward_overlap(prev)
