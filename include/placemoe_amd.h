@@ -224,7 +224,10 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
                                   int64_t I, void* dG1, pmx_stream_t stream);
 
 /* Ragged-K grouped GEMM (weight gradient):
- *   C[g] = bf16(A[rows of g]^T @ B[rows of g]),  A [rows,M], B [rows,N], C [G,M,N];
+ *   C[g] = bf16(A[rows of g]^T @ B[rows of g]),  A [K,M], B [K,N], C [G,M,N],
+ * K = the rows of A and B (offsets[G] <= K); it selects the addressing: up to
+ * 2 GiB per operand, one descriptor per group; beyond, 64-bit windows rebased
+ * per 64-row K-tile (any group size);
  * a group with no rows stores zeros.  Rows m >= c_split of C[g] go to C1
  * (split fc1 gradients), else to C0; pass C1 = NULL for one tensor.
  * A and B must be valid device pointers even when every group is empty
@@ -233,8 +236,8 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
  * Replaces group_gemm_same_mn(transpose_a=True)
  * (veomni/ops/kernels/moe/_kernels/kernel/group_gemm.py:370-410). */
 int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int32_t G,
-                      int64_t M, int64_t N, void* C0, void* C1, int64_t c_copy_stride,
-                      int64_t c_split, pmx_stream_t stream);
+                      int64_t K, int64_t M, int64_t N, void* C0, void* C1,
+                      int64_t c_copy_stride, int64_t c_split, pmx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
 /* Replica-gradient fold                                                     */

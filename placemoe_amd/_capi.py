@@ -86,7 +86,7 @@ SIGNATURES = {
     ),
     "pmx_group_gemm_tn": (
         c_int,
-        [c_void_p, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64,
          c_void_p],
     ),
     "pmx_replica_fold": (

@@ -79,7 +79,7 @@ struct GemmParams {
   RowSrc a, b;
   const int32_t* offsets;
   int32_t G;
-  int64_t M, N, K;  // ragged-M kinds: N, K used.  KIND_TN: M, N used.
+  int64_t M, N, K;  // ragged-M kinds: N, K used.  KIND_TN: M, N, and K = rows of A and B.
   int64_t I;        // SwiGLU width for KIND_FC1 and KIND_NNS
   bf16_t* c0;
   bf16_t* c1;
@@ -222,7 +222,17 @@ __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt,
 template <int W, bool REBASE, int Q0B = 0, int Q0E = loads_per_wave<W>(), bool FAST = false>
 __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt, bool live, int wave) {
   constexpr int ROWS = 1024 / (2 * W);
-  if constexpr (FAST && !REBASE) {
+  if constexpr (FAST && REBASE) {
+    // Weight gradient whose operands fit 31-bit offsets: one descriptor per
+    // group (rows past its end fail the range check), the K-tile advance in
+    // the scalar offset.
+    const uint32_t soff = (uint32_t)kt * (uint32_t)BK * op.ldb;
+#pragma unroll
+    for (int q0 = Q0B; q0 < Q0E; ++q0) {
+      const int q = q0 * NWAVES + wave;
+      dma16(op.r0, lds + q * 1024, op.voff[q0], soff);
+    }
+  } else if constexpr (FAST && !REBASE) {
 #pragma unroll
     for (int q0 = Q0B; q0 < Q0E; ++q0) {
       const int q = q0 * NWAVES + wave;
@@ -269,7 +279,7 @@ __device__ __forceinline__ void issue_stage(char* stage, const Tile<KIND, BM>& t
   char* As = stage;
   char* Bs = stage + BM * BK * 2;
   if constexpr (PART != 1) {
-    if constexpr (a_is_mn<KIND>()) dma_mn<BM, true>(As, tc.A, kt, live, wave);
+    if constexpr (a_is_mn<KIND>()) dma_mn<BM, true, 0, loads_per_wave<BM>(), FAST>(As, tc.A, kt, live, wave);
     else dma_kc<BM, false, 0, loads_per_wave<BM>(), FAST>(As, tc.A, kt, live, wave);
   }
   if constexpr (PART != 0) {
@@ -282,7 +292,7 @@ __device__ __forceinline__ void issue_stage(char* stage, const Tile<KIND, BM>& t
 template <int KIND, int BM, bool FAST, int OPER, int Q0>
 __device__ __forceinline__ void issue_one(char* stage, const Tile<KIND, BM>& tc, int32_t kt, bool live, int wave) {
   if constexpr (OPER == 0) {
-    if constexpr (a_is_mn<KIND>()) dma_mn<BM, true, Q0, Q0 + 1>(stage, tc.A, kt, live, wave);
+    if constexpr (a_is_mn<KIND>()) dma_mn<BM, true, Q0, Q0 + 1, FAST>(stage, tc.A, kt, live, wave);
     else dma_kc<BM, false, Q0, Q0 + 1, FAST>(stage, tc.A, kt, live, wave);
   } else {
     char* Bs = stage + BM * BK * 2;
@@ -654,8 +664,9 @@ __device__ __forceinline__ void mn_offsets(Operand& op, int wave, int lane, int6
   }
 }
 
-// Describe the operands of one output tile.
-template <int KIND, int BM>
+// Describe the operands of one output tile.  FAST weight gradients address
+// each operand through one descriptor over the group's rows.
+template <int KIND, int BM, bool FAST = false>
 __device__ __forceinline__ void setup_operands(const GemmParams& P, Tile<KIND, BM>& tc, int wave, int lane) {
   // Opaque lane: keeps the per-lane offset arithmetic here (see epilogue).
   asm volatile("" : "+v"(lane));
@@ -671,8 +682,13 @@ __device__ __forceinline__ void setup_operands(const GemmParams& P, Tile<KIND, B
     tc.B.bytes = (uint64_t)rows * (uint64_t)P.b.ld * 2u;
     mn_offsets<BM, true>(tc.A, wave, lane, (int64_t)ti.mtile * BM, P.M, 0);
     mn_offsets<BN, true>(tc.B, wave, lane, (int64_t)ti.ntile * BN, P.N, 0);
-    rebase_ktile(tc.A, 0, true);
-    rebase_ktile(tc.B, 0, true);
+    if constexpr (FAST) {
+      tc.A.r0 = make_rsrc(tc.A.base, tc.A.bytes);
+      tc.B.r0 = make_rsrc(tc.B.base, tc.B.bytes);
+    } else {
+      rebase_ktile(tc.A, 0, true);
+      rebase_ktile(tc.B, 0, true);
+    }
   } else {
     const int64_t rows = ti.row_end - ti.row0 < BM ? ti.row_end - ti.row0 : BM;
     const bf16_t* a0 = P.a.p0 + (int64_t)ti.row0 * P.a.ld;
@@ -926,11 +942,13 @@ __device__ __noinline__ int32_t build_wgrad_order(const GemmParams& P, int32_t* 
 // FAST (ragged-M kinds): K is a multiple of 64 and the dgrad weights are one
 // tensor, so the loads need no K-tail masking, no split test and no `live`
 // test (dma_kc, dma_mn; the slots past the block's last K-tile re-load the
-// first K-tile of its last tile, whose data is never multiplied).
+// first K-tile of its last tile, whose data is never multiplied).  FAST
+// weight gradient: every operand row lies within 31-bit offsets, so each
+// group is one descriptor and a K-tile is a scalar offset into it, instead of
+// a 64-bit window rebased per K-tile.
 template <int KIND, int BM, bool BAL = false, bool FAST = false>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P) {
   static_assert(!BAL || KIND == KIND_TN, "the balanced order is the weight gradient's");
-  static_assert(!FAST || KIND != KIND_TN, "the weight gradient has no fast variant");
   static_assert(BM == 256, "the schedule below is written for 256 x 256 tiles");
   static_assert(BK == pmx::kKTileRows, "wgrad K-tile windows are 64 rows deep");
   constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
@@ -1037,11 +1055,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   int32_t i_kt = 0;
   bool i_live = true;
   it.i = cur;
-  setup_operands<KIND, BM>(P, it, wave, lane);
+  setup_operands<KIND, BM, FAST>(P, it, wave, lane);
   auto advance_issue = [&]() {
     if (!i_live) return;
     if (++i_kt < it.i.nk) {
-      if constexpr (KIND == KIND_TN) {
+      if constexpr (KIND == KIND_TN && !FAST) {
         rebase_ktile(it.A, i_kt, true);
         rebase_ktile(it.B, i_kt, true);
       }
@@ -1050,12 +1068,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     i_kt = 0;
     while (tile_at(++i_seq, it.i)) {
       if (it.i.nk > 0) {
-        setup_operands<KIND, BM>(P, it, wave, lane);
+        setup_operands<KIND, BM, FAST>(P, it, wave, lane);
         return;
       }
     }
     i_live = false;
-    if constexpr (KIND == KIND_TN) {
+    if constexpr (KIND == KIND_TN && !FAST) {
       rebase_ktile(it.A, 0, false);
       rebase_ktile(it.B, 0, false);
     }
@@ -1170,6 +1188,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   }
 }
 
+// Buffer offsets are 32-bit: one descriptor covers at most 2 GiB.
+bool fits_rsrc(int64_t rows, int64_t ld) { return rows * ld * 2 < (int64_t)0x7fffffff; }
+
 int g_num_cus = 0;
 
 int grid_size() {
@@ -1194,8 +1215,15 @@ int launch(const GemmParams& P, hipStream_t stream) {
   const int grid = grid_size();
   if (grid <= 0) return PMX_ERR_HIP;
   if constexpr (KIND == KIND_TN) {
-    if (grid == kNumXcd * kBandTiles && P.G <= NTHREADS) {
+    // FAST: every row of both operands within 31-bit offsets (P.K = their rows).
+    const bool fast = fits_rsrc(P.K, P.M) && fits_rsrc(P.K, P.N);
+    const bool bal = grid == kNumXcd * kBandTiles && P.G <= NTHREADS;
+    if (bal && fast) {
+      grouped_gemm_kernel<KIND_TN, kBM, true, true><<<grid, NTHREADS, 0, stream>>>(P);
+    } else if (bal) {
       grouped_gemm_kernel<KIND_TN, kBM, true><<<grid, NTHREADS, 0, stream>>>(P);
+    } else if (fast) {
+      grouped_gemm_kernel<KIND_TN, kBM, false, true><<<grid, NTHREADS, 0, stream>>>(P);
     } else {
       grouped_gemm_kernel<KIND_TN, kBM><<<grid, NTHREADS, 0, stream>>>(P);
     }
@@ -1222,8 +1250,6 @@ RowSrc one(const void* p, int64_t gs, int64_t ld) {
   return s;
 }
 
-// Buffer offsets are 32-bit: one descriptor covers at most 2 GiB.
-bool fits_rsrc(int64_t rows, int64_t ld) { return rows * ld * 2 < (int64_t)0x7fffffff; }
 
 }  // namespace
 
@@ -1349,9 +1375,9 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
   return launch<KIND_NNS>(P, stream);
 }
 
-int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
-                      void* C0, void* C1, int64_t c_copy_stride, int64_t c_split, pmx_stream_t stream) {
-  if (G <= 0 || G > kMaxGroups || M <= 0 || N <= 0) return PMX_ERR_ARG;
+int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t K, int64_t M,
+                      int64_t N, void* C0, void* C1, int64_t c_copy_stride, int64_t c_split, pmx_stream_t stream) {
+  if (G <= 0 || G > kMaxGroups || K < 0 || M <= 0 || N <= 0) return PMX_ERR_ARG;
   if (M % 8 || N % 8) return PMX_ERR_SHAPE;
   // One K-tile (64 rows) of either operand lies within one descriptor; the
   // group as a whole may span any number of bytes (rebased per K-tile).
@@ -1363,6 +1389,7 @@ int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int3
   P.b = one(B, 0, N);
   P.offsets = offsets;
   P.G = G;
+  P.K = K;
   P.M = M;
   P.N = N;
   P.c0 = static_cast<bf16_t*>(C0);

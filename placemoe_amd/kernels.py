@@ -380,6 +380,8 @@ def group_gemm_tn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, split
     _bf16("a", a)
     _bf16("b", b)
     M, N = a.shape[1], b.shape[1]
+    K = a.shape[0]
+    assert b.shape[0] == K, "a and b must have the same rows"
     G = offsets.numel() - 1
     if a.shape[0] == 0:
         # No rows at all (an empty micro-batch): every group is empty, so every C[g] is zero.
@@ -389,14 +391,14 @@ def group_gemm_tn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, split
     if split is None:
         c0 = torch.empty((G, M, N), dtype=a.dtype, device=dev)
         _capi.call(
-            "pmx_group_gemm_tn", _ptr(a), _ptr(b), _ptr(offsets), G, M, N, _ptr(c0), None, M * N, 0, _stream(dev)
+            "pmx_group_gemm_tn", _ptr(a), _ptr(b), _ptr(offsets), G, K, M, N, _ptr(c0), None, M * N, 0, _stream(dev)
         )
         return c0
     assert M - split == split, "split gradients must have equal halves"
     c0 = torch.empty((G, split, N), dtype=a.dtype, device=dev)
     c1 = torch.empty((G, split, N), dtype=a.dtype, device=dev)
     _capi.call(
-        "pmx_group_gemm_tn", _ptr(a), _ptr(b), _ptr(offsets), G, M, N, _ptr(c0), _ptr(c1), split * N, split,
+        "pmx_group_gemm_tn", _ptr(a), _ptr(b), _ptr(offsets), G, K, M, N, _ptr(c0), _ptr(c1), split * N, split,
         _stream(dev),
     )
     return c0, c1
