@@ -44,9 +44,9 @@ PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 # cannot be read from inside a timed run, so the figure is carried here; other
 # workloads report traffic null.
 MEASURED_TRAFFIC_BYTES = {
-    ("dsv3", "fc1_fwd"): (6990 + 877) * 2**20,
-    ("dsv3", "fc1_wgrad"): (5416 + 896) * 2**20,
-    ("dsv3", "fc1_dgrad"): (6825 + 896) * 2**20,
+    ("dsv3", "fc1_fwd"): (7249 + 892) * 2**20,
+    ("dsv3", "fc1_wgrad"): (5782 + 896) * 2**20,
+    ("dsv3", "fc1_dgrad"): (6931 + 896) * 2**20,
     ("qwen3", "fc1_fwd"): (2433 + 654) * 2**20,
     ("qwen3", "fc1_wgrad"): (1338 + 960) * 2**20,
     ("qwen3", "fc1_dgrad"): (2098 + 512) * 2**20,
