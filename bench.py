@@ -47,9 +47,9 @@ MEASURED_TRAFFIC_BYTES = {
     ("dsv3", "fc1_fwd"): (7249 + 892) * 2**20,
     ("dsv3", "fc1_wgrad"): (5782 + 896) * 2**20,
     ("dsv3", "fc1_dgrad"): (6931 + 896) * 2**20,
-    ("qwen3", "fc1_fwd"): (2433 + 654) * 2**20,
-    ("qwen3", "fc1_wgrad"): (1338 + 960) * 2**20,
-    ("qwen3", "fc1_dgrad"): (2098 + 512) * 2**20,
+    ("qwen3", "fc1_fwd"): (2451 + 653) * 2**20,
+    ("qwen3", "fc1_wgrad"): (1345 + 960) * 2**20,
+    ("qwen3", "fc1_dgrad"): (2083 + 512) * 2**20,
 }
 
 # Entry-point call order inside one step; repeated names are told apart by
