@@ -1,8 +1,10 @@
 """Floating-point parity at the full benchmark shapes, stage by stage.
 
-Every kernel of the layer runs at the shape ``bench.py`` times (config 3:
-65536 rows over 16 copies of 1.2k-19.4k rows, H=7168, I=2048; config 4:
-T=32768, K=4, H=4096, I=1536, 96 copies with empty and tiny ones).  Each
+Every kernel of the layer runs at the full shape of a benchmark config
+(config 2: T=16384, K=8, H=2048, I=768, 160 copies; config 3: 65536 rows over
+16 copies of 1.2k-19.4k rows, H=7168, I=2048; config 4: T=32768, K=4, H=4096,
+I=1536, 96 copies with empty and tiny ones; config 5: the config-2 shape over
+256 copies of 128 experts).  Each
 stage is then checked on the CPU with the oracle on a sample, fed with that
 stage's own GPU inputs (so a stage is judged on its own rounding):
 
@@ -75,7 +77,8 @@ def _check_wgrad(name, grad, a, b, offsets, groups, rng, tiles_per_group=4):
             assert_bf16_close(got, ref, name=f"{name} copy {g} ({e - s} rows) tile ({m0},{n0})")
 
 
-@pytest.mark.parametrize("config,per_group,tokens_checked", [("dsv3", 256, 2048), ("skew", 48, 2048)])
+@pytest.mark.parametrize("config,per_group,tokens_checked",
+                         [("qwen3", 24, 2048), ("dsv3", 256, 2048), ("skew", 48, 2048), ("fold", 16, 2048)])
 def test_full_shape_stagewise(cuda, config, per_group, tokens_checked):
     torch.set_num_threads(min(16, torch.get_num_threads()))
     wl = make_workload(config, device=cuda)
