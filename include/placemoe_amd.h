@@ -229,7 +229,10 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
  * 2 GiB per operand, one descriptor per group; beyond, 64-bit windows rebased
  * per 64-row K-tile (any group size);
  * a group with no rows stores zeros.  Rows m >= c_split of C[g] go to C1
- * (split fc1 gradients), else to C0; pass C1 = NULL for one tensor.
+ * (split fc1 gradients, row m - c_split), else to C0; pass C1 = NULL for one
+ * tensor.  Copy g of either tensor starts c_copy_stride elements after copy
+ * g - 1 (a multiple of 8, at least the rows the tensor holds times N); A, B,
+ * C0 and C1 are 16-byte aligned (PMX_ERR_SHAPE / PMX_ERR_ARG otherwise).
  * A and B must be valid device pointers even when every group is empty
  * (PMX_ERR_ARG otherwise); with no rows at all the caller can skip the call,
  * since every C[g] is zero.

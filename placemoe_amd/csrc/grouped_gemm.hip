@@ -1383,7 +1383,12 @@ int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int3
   // group as a whole may span any number of bytes (rebased per K-tile).
   if (!fits_rsrc(BK, M) || !fits_rsrc(BK, N)) return PMX_ERR_SHAPE;
   if (!A || !B || !offsets || !C0) return PMX_ERR_ARG;
-  if (!a16(A) || !a16(B)) return PMX_ERR_SHAPE;
+  if (C1 && (c_split <= 0 || c_split >= M)) return PMX_ERR_ARG;
+  // 16-byte row segments of C: both tensors aligned, copies 8-element aligned
+  // and apart by at least the rows each tensor holds (no two copies overlap).
+  if (!a16(A) || !a16(B) || !a16(C0) || (C1 && !a16(C1)) || c_copy_stride % 8) return PMX_ERR_SHAPE;
+  const int64_t c_rows = C1 ? (c_split > M - c_split ? c_split : M - c_split) : M;
+  if (G > 1 && c_copy_stride < c_rows * N) return PMX_ERR_ARG;
   GemmParams P = {};
   P.a = one(A, 0, M);
   P.b = one(B, 0, N);
@@ -1397,7 +1402,6 @@ int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int3
   P.cgs = c_copy_stride;
   P.ldc = N;
   P.csplit = C1 ? c_split : INT64_MAX;
-  if (C1 && (c_split <= 0 || c_split >= M)) return PMX_ERR_ARG;
   return launch<KIND_TN>(P, stream);
 }
 

@@ -92,3 +92,19 @@ def test_size_limits_rejected_before_any_launch():
         _capi.PMX_ERR_ARG
     assert lib.pmx_replica_exchange_unpack(dummy, 0, 64, 4, 1, dummy, dummy, 1, dummy, None, None, None, dummy,
                                            None) == _capi.PMX_ERR_ARG
+
+
+def test_wgrad_output_layout_rejected_before_any_launch():
+    """The weight gradient's output copies must be 16-byte aligned, 8-element
+    strided and must not overlap; each mistake is refused on the host."""
+    lib = _capi.load()
+    p = ctypes.c_void_p(256)
+    tn = lib.pmx_group_gemm_tn
+    M, N, G, K = 64, 64, 2, 128
+    assert tn(p, p, p, G, K, M, N, ctypes.c_void_p(258), None, M * N, 0, None) == _capi.PMX_ERR_SHAPE
+    assert tn(p, p, p, G, K, M, N, p, None, M * N + 4, 0, None) == _capi.PMX_ERR_SHAPE
+    assert tn(p, p, p, G, K, M, N, p, None, M * N - 8, 0, None) == _capi.PMX_ERR_ARG
+    assert tn(p, p, p, G, K, M, N, p, ctypes.c_void_p(264), (M // 2) * N, M // 2, None) == _capi.PMX_ERR_SHAPE
+    assert tn(p, p, p, G, K, M, N, p, p, (M // 2) * N, 0, None) == _capi.PMX_ERR_ARG
+    assert tn(p, p, p, G, K, M, N, p, p, (M // 2) * N, M, None) == _capi.PMX_ERR_ARG
+    assert tn(p, p, p, G, K, M, N, p, p, (M // 2) * N - 8, M // 2, None) == _capi.PMX_ERR_ARG
