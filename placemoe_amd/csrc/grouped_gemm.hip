@@ -302,6 +302,36 @@ __device__ __forceinline__ void issue_one(char* stage, const Tile<KIND, BM>& tc,
 }
 
 
+// RS: piece Q0 (A pieces 0 .. QA-1, then B) of this wave's share of K-tile
+// kt, loaded into a register with the addressing of the buffer->LDS
+// instruction it replaces (FAST ragged-M kinds), and its store to the LDS
+// position that instruction fills.
+template <int KIND, int BM, int PIECE>
+__device__ __forceinline__ uint4 load_piece(const Tile<KIND, BM>& tc, int32_t kt, int wave) {
+  constexpr int QA = loads_per_wave<BM>();
+  if constexpr (PIECE < QA) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(tc.A.r0, tc.A.voff[PIECE],
+                                                                          (uint32_t)kt * (BK * 2), 0));
+  } else {
+    constexpr int Q0 = PIECE - QA;
+    uint32_t soff;
+    if constexpr (b_is_mn<KIND>()) {
+      constexpr int ROWS = 1024 / (2 * BN);
+      soff = ((uint32_t)kt * BK + (uint32_t)((Q0 * NWAVES + wave) * ROWS)) * tc.B.ldb;
+    } else {
+      soff = (uint32_t)kt * (BK * 2);
+    }
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(tc.B.r0, tc.B.voff[Q0], soff, 0));
+  }
+}
+template <int BM, int PIECE>
+__device__ __forceinline__ void store_piece(char* stage, int wave, int lane, const uint4& v) {
+  constexpr int QA = loads_per_wave<BM>();
+  char* base = PIECE < QA ? stage : stage + BM * BK * 2;
+  constexpr int Q0 = PIECE < QA ? PIECE : PIECE - QA;
+  *reinterpret_cast<uint4*>(base + (Q0 * NWAVES + wave) * 1024 + lane * 16) = v;
+}
+
 // Fragment of a K-contiguous tile: lane l holds row (rb + l%32), k = ks*16 + (l/32)*8 + 0..7.
 __device__ __forceinline__ bf16x8_t frag_kc(const char* t, int rb, int ks, int lane) {
   const int row = rb + (lane & 31);
@@ -946,9 +976,18 @@ __device__ __noinline__ int32_t build_wgrad_order(const GemmParams& P, int32_t* 
 // weight gradient: every operand row lies within 31-bit offsets, so each
 // group is one descriptor and a K-tile is a scalar offset into it, instead of
 // a 64-bit window rebased per K-tile.
-template <int KIND, int BM, bool BAL = false, bool FAST = false>
+// RS (FAST fc1, fc2 and fc1 dgrad): no buffer->LDS loads.  Each of the
+// wave's eight 1 KB pieces of a K-tile passes through one register: at its
+// own point of K-tile p (one every four MFMA groups) the piece of K-tile p+1
+// is written to the refill stage and the register re-loaded with K-tile
+// p+2, so every load has a whole K-tile to land and the loads are spread
+// over the K-tile instead of crowding its first half; the compiler tracks
+// these loads, and the end of a K-tile waits only for LDS.
+template <int KIND, int BM, bool BAL = false, bool FAST = false, bool RS = false>
 __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P) {
   static_assert(!BAL || KIND == KIND_TN, "the balanced order is the weight gradient's");
+  static_assert(!RS || (FAST && (KIND == KIND_FC1 || KIND == KIND_NT || KIND == KIND_NN)),
+                "register-staged operands: FAST ragged-M kinds without the SwiGLU backward");
   static_assert(BM == 256, "the schedule below is written for 256 x 256 tiles");
   static_assert(BK == pmx::kKTileRows, "wgrad K-tile windows are 64 rows deep");
   constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
@@ -1083,12 +1122,32 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     advance_issue();
   };
 
-  // Prologue: the first K-tile lands in stage 0, then the second is issued.
-  issue_next(lds);
-  wait_loads<0>();
-  block_barrier();
+  // RS: one register per piece of this wave's share of a K-tile.  During
+  // K-tile p each piece is written to the refill stage (K-tile p + 1, loaded
+  // a K-tile earlier) and at once re-loaded with K-tile p + 2, at evenly
+  // spaced points of the K-tile, so every load has a whole K-tile to land.
+  constexpr int NPC = RS ? QA + QB : 1;
+  uint4 rg[NPC];
   int cs = 0;  // stage of the K-tile being multiplied
-  issue_next(lds + STAGE_BYTES);
+  if constexpr (RS) {
+    static_for<0, NPC>([&](auto q) __attribute__((always_inline)) {
+      rg[decltype(q)::value] = load_piece<KIND, BM, decltype(q)::value>(it, i_kt, wave);
+    });
+    advance_issue();
+    static_for<0, NPC>([&](auto q) __attribute__((always_inline)) {
+      store_piece<BM, decltype(q)::value>(lds, wave, lane, rg[decltype(q)::value]);
+      rg[decltype(q)::value] = load_piece<KIND, BM, decltype(q)::value>(it, i_kt, wave);
+    });
+    advance_issue();
+    wait_lds();
+    block_barrier();
+  } else {
+    // Prologue: the first K-tile lands in stage 0, then the second is issued.
+    issue_next(lds);
+    wait_loads<0>();
+    block_barrier();
+    issue_next(lds + STAGE_BYTES);
+  }
 
   // Per k-step: NM MFMAs, one per pinned group, and NR fragment reads, two
   // per group in the first groups.  The next K-tile's QA + QB loads go one
@@ -1111,14 +1170,25 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       read_frag<KIND, BM, frag_order(2 * j + 1)>(stage, decltype(ks)::value, wm, wn, lane, f);
     }
   };
+  // RS: piece i is written and re-loaded at group RSP * i of the K-tile.
+  constexpr int RSP = RS ? 4 * NF / NPC : 1;
+  auto rs_piece = [&](auto pc, char* refill) __attribute__((always_inline)) {
+    constexpr int q = decltype(pc)::value;
+    store_piece<BM, q>(refill, wave, lane, rg[q]);
+    rg[q] = load_piece<KIND, BM, q>(it, i_kt, wave);
+  };
   // k-step KS of the current K-tile: MFMAs of k-step KS-1 (fragments `fm`)
   // interleaved with the reads of k-step KS into `fr`, and, with LOADS, the
-  // loads of the next K-tile that fall into this k-step's groups.
+  // loads of the next K-tile that fall into this k-step's groups (RS: the
+  // pieces that fall into them).
   auto kstep = [&](auto ks, auto loads, auto oper, const char* stage, char* refill, const Frags<BM>& fm,
                    Frags<BM>& fr) __attribute__((always_inline)) {
     static_for<0, NF>([&](auto jj) __attribute__((always_inline)) {
       constexpr int j = decltype(jj)::value;
-      if constexpr (decltype(loads)::value) {
+      if constexpr (RS) {
+        constexpr int slot = decltype(ks)::value * NF + j;
+        if constexpr (slot % RSP == 0 && slot / RSP < NPC) rs_piece(Int<slot / RSP>{}, refill);
+      } else if constexpr (decltype(loads)::value) {
         static_for<0, QA + QB>([&](auto ll) __attribute__((always_inline)) {
           constexpr int l = decltype(ll)::value;
           if constexpr (SPREAD * l == decltype(ks)::value * NF + j) {
@@ -1141,6 +1211,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       // K-tile 0: no MFMAs pending, and the next K-tile is already in flight.
       const char* stage = lds + cs * STAGE_BYTES;
       char* refill = lds + (cs ^ 1) * STAGE_BYTES;
+      if constexpr (RS) {
+        // the pieces of k-step 0's groups (that k-step's MFMAs belong to the previous tile)
+        static_for<0, NPC>([&](auto pc) __attribute__((always_inline)) {
+          if constexpr (decltype(pc)::value * RSP < NF) rs_piece(pc, refill);
+        });
+      }
       static_for<0, NR>([&](auto jj) __attribute__((always_inline)) {
         constexpr int j = decltype(jj)::value;
         read_frag<KIND, BM, frag_order(j)>(stage, 0, wm, wn, lane, f0);
@@ -1148,7 +1224,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       kstep(Int<1>{}, Int<0>{}, Int<0>{}, stage, refill, f0, f1);
       kstep(Int<2>{}, Int<0>{}, Int<0>{}, stage, refill, f1, f0);
       kstep(Int<3>{}, Int<0>{}, Int<0>{}, stage, refill, f0, f1);
-      wait_loads_lds<0>();
+      if constexpr (RS) {
+        advance_issue();
+        wait_lds();
+      } else {
+        wait_loads_lds<0>();
+      }
       block_barrier();
       cs ^= 1;
     }
@@ -1160,7 +1241,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       kstep(Int<2>{}, Int<1>{}, Int<0>{}, stage, refill, f1, f0);
       kstep(Int<3>{}, Int<1>{}, Int<0>{}, stage, refill, f0, f1);
       advance_issue();
-      wait_loads_lds<0>();
+      if constexpr (RS) {
+        wait_lds();
+      } else {
+        wait_loads_lds<0>();
+      }
       block_barrier();
       cs ^= 1;
     }
@@ -1183,8 +1268,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
       wait_loads<0>();
       return;
     }
-    wait_lds();
-    issue_next(lds + (cs ^ 1) * STAGE_BYTES);
+    if constexpr (!RS) {
+      wait_lds();
+      issue_next(lds + (cs ^ 1) * STAGE_BYTES);
+    }
   }
 }
 
@@ -1209,6 +1296,7 @@ int grid_size() {
 // bounds this kernel, so that outweighs the coarser padding of ragged groups.
 // Each wave's 128 x 64 share takes 128 accumulator registers per lane.
 constexpr int kBM = 256;
+constexpr int64_t kRsMaxRowsPerCopy = 8 * kBM;
 
 template <int KIND>
 int launch(const GemmParams& P, hipStream_t stream) {
@@ -1229,10 +1317,23 @@ int launch(const GemmParams& P, hipStream_t stream) {
     }
   } else {
     // FAST: K a multiple of 64, dgrad weights not split (P.b.split >= K).
-    if (P.K % BK == 0 && (KIND != KIND_NN || P.b.split >= P.K)) {
-      grouped_gemm_kernel<KIND, kBM, false, true><<<grid, NTHREADS, 0, stream>>>(P);
-    } else {
+    // RS (register-staged operands): fc1 and fc2 always; the fc1 dgrad when
+    // the copies are small (under 8 m-tiles of rows on average), where each
+    // weight strip serves few tiles and its loads wait on memory - with a
+    // few large copies the DMA path is faster (it spends less power).
+    const bool fast = P.K % BK == 0 && (KIND != KIND_NN || P.b.split >= P.K);
+    if (!fast) {
       grouped_gemm_kernel<KIND, kBM><<<grid, NTHREADS, 0, stream>>>(P);
+    } else if constexpr (KIND == KIND_FC1 || KIND == KIND_NT) {
+      grouped_gemm_kernel<KIND, kBM, false, true, true><<<grid, NTHREADS, 0, stream>>>(P);
+    } else if constexpr (KIND == KIND_NN) {
+      if (P.M < kRsMaxRowsPerCopy * (int64_t)P.G) {
+        grouped_gemm_kernel<KIND, kBM, false, true, true><<<grid, NTHREADS, 0, stream>>>(P);
+      } else {
+        grouped_gemm_kernel<KIND, kBM, false, true><<<grid, NTHREADS, 0, stream>>>(P);
+      }
+    } else {
+      grouped_gemm_kernel<KIND, kBM, false, true><<<grid, NTHREADS, 0, stream>>>(P);
     }
   }
   PMX_LAUNCH_CHECK();
