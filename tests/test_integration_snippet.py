@@ -1,6 +1,6 @@
-"""The registration snippet INTEGRATION.md tells a maintainer to add to the
-reference (its section 3) runs as written: executed in a namespace that
-stands in for the reference module (veomni/ops/kernels/moe/__init__.py:
+"""The registration snippet that the repository's integration guide tells a
+maintainer to add to the reference runs as written: executed in a namespace
+that stands in for the reference module (veomni/ops/kernels/moe/__init__.py:
 its KERNEL_REGISTRY, KernelSpec, HardwareRequirement, module-level
 ``_fused_moe_forward`` and ``apply_veomni_fused_moe_patch``), it registers
 the "hip" backend and lets the patch function bind it.  Hardware is mocked."""
@@ -22,7 +22,7 @@ def _section_3_snippet() -> str:
     start = text.index("## 3. Registering the backend with the reference")
     end = text.index("\n## 4.", start)
     blocks = re.findall(r"```python\n(.*?)```", text[start:end], flags=re.S)
-    assert len(blocks) == 1, "section 3 holds one python snippet"
+    assert len(blocks) == 1, "the registration section holds one python snippet"
     return blocks[0]
 
 
