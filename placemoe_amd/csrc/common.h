@@ -25,6 +25,21 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) { return __builtin_bit_
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// Two fp32 -> a bf16 pair (a in the low half) in one v_cvt_pk_bf16_f32, with
+// the same rounding as f32_to_bf16.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
+// round_bf16 of two values through one conversion.
+__device__ __forceinline__ void round2_bf16(float& a, float& b) {
+  const uint32_t p = pack2(a, b);
+  a = __uint_as_float(p << 16);
+  b = __uint_as_float(p & 0xffff0000u);
+}
+
 // Unpack / pack 8 bf16 held in a uint4 (element 2j in the low half of word j).
 __device__ __forceinline__ void unpack8(const uint4 v, float* f) {
   f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xffff0000u);
@@ -34,12 +49,7 @@ __device__ __forceinline__ void unpack8(const uint4 v, float* f) {
 }
 
 __device__ __forceinline__ uint4 pack8(const float* f) {
-  uint4 v;
-  v.x = f32_to_bf16(f[0]) | (f32_to_bf16(f[1]) << 16);
-  v.y = f32_to_bf16(f[2]) | (f32_to_bf16(f[3]) << 16);
-  v.z = f32_to_bf16(f[4]) | (f32_to_bf16(f[5]) << 16);
-  v.w = f32_to_bf16(f[6]) | (f32_to_bf16(f[7]) << 16);
-  return v;
+  return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
 }
 
 // 16-byte streaming (non-temporal) global load and store, for row data that
@@ -61,8 +71,13 @@ __device__ __forceinline__ void st_row(void* p, const uint4 v) {
   else *reinterpret_cast<uint4*>(p) = v;
 }
 
-__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + __expf(-x)); }
-__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// sigmoid(x) = 1 / (1 + exp(-x)) with the hardware exponential (__expf) and
+// reciprocal (v_rcp_f32, 1 ulp) instead of an IEEE division, and silu(x) =
+// x * sigmoid(x): a few ulp of fp32 from the correctly rounded quotient, which
+// the kernels' outputs then round to bf16.  The divisions were the bulk of the
+// GEMM epilogues' VALU work, which holds the matrix cores idle.
+__device__ __forceinline__ float sigmoid_f32(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ float silu_f32(float x) { return x * sigmoid_f32(x); }
 
 // Wave-wide sum (64 lanes) with cross-lane shuffles.
 __device__ __forceinline__ float wave_sum(float v) {

@@ -402,13 +402,15 @@ __device__ __forceinline__ void read_frag(const char* stage, int ks, int wm, int
 // read_frag: A fragments 0 .. MT-1, B fragments MT .. MT+NTT-1.
 constexpr int frag_order(int i) { return i == 0 ? 0 : i <= NTT ? MT + i - 1 : i - NTT; }
 
-// MFMAs I .. I+N-1 of a k-step (index mt * NTT + nt).
-template <int BM, int I, int N>
+// MFMAs I .. I+N-1 of a k-step (index mt * NTT + nt).  FIRST: the tile's
+// first k-step, whose MFMAs start from zero (an inline-constant accumulator
+// operand) instead of from cleared registers.
+template <int BM, int I, int N, bool FIRST = false>
 __device__ __forceinline__ void mma_some(const Frags<BM>& f, f32x16_t (&acc)[MT][NTT]) {
 #pragma unroll
   for (int x = I; x < I + N; ++x)
-    acc[x / NTT][x % NTT] =
-        __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[x % NTT], f.a[x / NTT], acc[x / NTT][x % NTT], 0, 0, 0);
+    acc[x / NTT][x % NTT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        f.b[x % NTT], f.a[x / NTT], FIRST ? f32x16_t{} : acc[x / NTT][x % NTT], 0, 0, 0);
 }
 
 template <int BM>
@@ -434,16 +436,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-template <int BM>
-__device__ __forceinline__ void zero_acc(f32x16_t (&acc)[MT][NTT]) {
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NTT; ++nt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
-}
-
 // The MFMAs take the B fragment as their first operand, so each accumulator
 // holds its 32 x 32 output tile transposed: element i of acc[mt][nt] in lane
 // l is output row l%32, column 8*(i/4) + 4*(l/32) + i%4.  A lane therefore
@@ -466,22 +458,28 @@ __device__ __forceinline__ void zero_acc(f32x16_t (&acc)[MT][NTT]) {
 // EPMergedFc1GroupGemm.backward, veomni/distributed/moe/moe_layer.py:453-482,
 // :479): dact is the bf16 dgrad output,
 //   s = bf16(silu(g)), d_silu = bf16(dact * u), sig = sigmoid(g)
-//   dgate = d_silu * sig * (1 + g * (1 - sig)),  dup = s * dact.
+//   dgate = d_silu * sig * (1 + g * (1 - sig)),  dup = s * dact,
+// with sig * (1 + g * (1 - sig)) evaluated as sig + silu(g) * (1 - sig) in
+// one fma (fp32 rounding differs from aten's order by a few ulp).
 __device__ __forceinline__ void swiglu_bwd8(const float* dact, const float* g, const float* u, float* dgate,
                                             float* dup) {
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const float s = round_bf16(silu_f32(g[q]));
-    const float d_silu = round_bf16(dact[q] * u[q]);
-    const float sig = sigmoid_f32(g[q]);
-    dgate[q] = d_silu * (sig * (1.0f + g[q] * (1.0f - sig)));
-    dup[q] = s * dact[q];
+  for (int q = 0; q < 8; q += 2) {
+    const float sig0 = sigmoid_f32(g[q]), sig1 = sigmoid_f32(g[q + 1]);
+    const float gs0 = g[q] * sig0, gs1 = g[q + 1] * sig1;
+    float s0 = gs0, s1 = gs1;
+    float d0 = dact[q] * u[q], d1 = dact[q + 1] * u[q + 1];
+    round2_bf16(s0, s1);
+    round2_bf16(d0, d1);
+    dgate[q] = d0 * __builtin_fmaf(gs0, 1.0f - sig0, sig0);
+    dgate[q + 1] = d1 * __builtin_fmaf(gs1, 1.0f - sig1, sig1);
+    dup[q] = s0 * dact[q];
+    dup[q + 1] = s1 * dact[q + 1];
   }
 }
 
-__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) {
-  return make_uint2(f32_to_bf16(a) | (f32_to_bf16(b) << 16), f32_to_bf16(c) | (f32_to_bf16(d) << 16));
-}
+__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) { return make_uint2(pack2(a, b), pack2(c, d)); }
+__device__ __forceinline__ uint2 acc4(const f32x16_t& a, int i) { return pack4(a[i], a[i + 1], a[i + 2], a[i + 3]); }
 
 // Byte offset, inside the stage, of byte `x` of row r (0..63) of the wave's staging area.
 __device__ __forceinline__ int epi_off(int wave, int r, int x) {
@@ -489,8 +487,8 @@ __device__ __forceinline__ int epi_off(int wave, int r, int x) {
   return ((r >> 3) * NWAVES + wave) * 1024 + (r & 7) * 128 + (chunk << 4) + (x & 15);
 }
 
-// Stage rows 64*half .. +63 of the wave's tile from `v(mt, nt, i)` (columns
-// 0 .. 32*NC-1 of the wave's 64), as bf16.
+// Stage rows 64*half .. +63 of the wave's tile (columns 0 .. 32*NC-1 of the
+// wave's 64) from `v(mt, nt, i)`: elements i .. i+3 of acc[mt][nt] as four bf16.
 template <int NC, typename F>
 __device__ __forceinline__ void stage_half(char* stage, int wave, int lane, int half, F v) {
   const int rl = lane & 31, h = lane >> 5;
@@ -503,13 +501,36 @@ __device__ __forceinline__ void stage_half(char* stage, int wave, int lane, int 
         const int mt = 2 * half + mtl;
         const int r = mtl * 32 + rl;
         const int col = nt * 32 + 8 * j + 4 * h;
-        *reinterpret_cast<uint2*>(stage + epi_off(wave, r, col * 2)) =
-            pack4(v(mt, nt, 4 * j), v(mt, nt, 4 * j + 1), v(mt, nt, 4 * j + 2), v(mt, nt, 4 * j + 3));
+        *reinterpret_cast<uint2*>(stage + epi_off(wave, r, col * 2)) = v(mt, nt, 4 * j);
       }
 }
 
 __device__ __forceinline__ uint4 staged_chunk(const char* stage, int wave, int r, int chunk) {
   return *reinterpret_cast<const uint4*>(stage + epi_off(wave, r, chunk * 16));
+}
+
+// Rows row0 .. row0+63 of a row-major bf16 tensor of `ld` elements per row
+// (one epilogue round) as a buffer descriptor that ends at row `row_end`, so
+// that the range check drops the loads (zeros) and stores of rows past the
+// tile's group: no 64-bit address arithmetic and no branch per store.  The
+// whole offset, row and column, is the 32-bit vector offset (kOOB for columns
+// past the tensor): the range check covers the vector offset only, not the
+// scalar one.
+struct OutWin {
+  __amdgpu_buffer_rsrc_t r;
+  uint32_t rowb;  // bytes per row
+};
+__device__ __forceinline__ OutWin out_window(const bf16_t* base, int64_t row0, int64_t row_end, int64_t ld) {
+  const int64_t rows = row_end - row0 < 0 ? 0 : (row_end - row0 > 64 ? 64 : row_end - row0);
+  return {make_rsrc(base + row0 * ld, (uint64_t)(rows * ld * 2)), (uint32_t)(ld * 2)};
+}
+constexpr int kCpolNT = 2;  // buffer instruction cache policy: non-temporal (streaming)
+// Row `row` further on from a lane's offset `voff`.
+__device__ __forceinline__ void win_store(const OutWin& w, uint32_t voff, uint32_t row, const uint4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{v.x, v.y, v.z, v.w}, w.r, voff + row * w.rowb, 0, kCpolNT);
+}
+__device__ __forceinline__ uint4 win_load(const OutWin& w, uint32_t voff, uint32_t row) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w.r, voff + row * w.rowb, 0, kCpolNT));
 }
 
 template <int KIND, int BM>
@@ -529,11 +550,17 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
   float wt[16];
   if constexpr (KIND == KIND_NT || KIND == KIND_NN) {
     if (mapped) {
+      // The wave's rows through descriptors that end at the group's last row.
+      const int64_t r0 = ti.row0 + wm * WROWS;
+      const int32_t nrows = (int32_t)(ti.row_end - r0 < 0 ? 0 : (ti.row_end - r0 > WROWS ? WROWS : ti.row_end - r0));
+      const __amdgpu_buffer_rsrc_t rt = make_rsrc(P.row_tok + r0, (uint64_t)nrows * 4);
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(P.row_w + r0, (uint64_t)nrows * 2);
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        const int64_t row = ti.row0 + wm * WROWS + (q >> 3) * 64 + (q & 7) * 8 + (lane >> 3);
-        dst[q] = row < ti.row_end ? P.row_tok[row] : -1;
-        if constexpr (KIND == KIND_NT) wt[q] = row < ti.row_end ? bf16_to_f32(P.row_w[row]) : 0.f;
+        const int r = (q >> 3) * 64 + (q & 7) * 8 + (lane >> 3);
+        const int32_t tok = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rt, (uint32_t)r * 4u, 0, 0);
+        dst[q] = r < nrows ? tok : -1;
+        if constexpr (KIND == KIND_NT) wt[q] = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rw, (uint32_t)r * 2u, 0, 0));
       }
     }
   }
@@ -545,65 +572,69 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
       // first both as bf16 GEMM outputs (gu), then act = bf16(bf16(silu(gate)) * up).
       const int64_t I = P.I;
       const int64_t j0 = (int64_t)ti.ntile * 128 + wn * 32;
-      stage_half<2>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      stage_half<2>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc4(acc[mt][nt], i); });
       const int cc = lane & 7;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int rl = q * 8 + (lane >> 3);
-        const int64_t row = ti.row0 + rb + rl;
-        const uint4 v = staged_chunk(stage, wave, rl, cc);
+      {
+        const OutWin w = out_window(P.gu, ti.row0 + rb, ti.row_end, 2 * I);
         const int64_t j = j0 + (cc & 3) * 8;
-        if (row < ti.row_end && j < I) st_stream(P.gu + row * 2 * I + (cc < 4 ? 0 : I) + j, v);
+        const uint32_t voff = j < I ? (uint32_t)(lane >> 3) * w.rowb + (uint32_t)((cc < 4 ? 0 : I) + j) * 2u : kOOB;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) win_store(w, voff, q * 8, staged_chunk(stage, wave, q * 8 + (lane >> 3), cc));
       }
       stage_half<1>(stage, wave, lane, half, [&](int mt, int, int i) {
-        return round_bf16(silu_f32(round_bf16(acc[mt][0][i]))) * round_bf16(acc[mt][1][i]);
+        float g[4], u[4];
+#pragma unroll
+        for (int k = 0; k < 4; k += 2) {
+          g[k] = acc[mt][0][i + k], g[k + 1] = acc[mt][0][i + k + 1];
+          u[k] = acc[mt][1][i + k], u[k + 1] = acc[mt][1][i + k + 1];
+          round2_bf16(g[k], g[k + 1]);
+          round2_bf16(u[k], u[k + 1]);
+          g[k] = silu_f32(g[k]), g[k + 1] = silu_f32(g[k + 1]);
+          round2_bf16(g[k], g[k + 1]);
+        }
+        return pack4(g[0] * u[0], g[1] * u[1], g[2] * u[2], g[3] * u[3]);
       });
       const int c4 = lane & 3;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int rl = q * 16 + (lane >> 2);
-        const int64_t row = ti.row0 + rb + rl;
-        const uint4 v = staged_chunk(stage, wave, rl, c4);
+      {
+        const OutWin w = out_window(P.act, ti.row0 + rb, ti.row_end, I);
         const int64_t j = j0 + c4 * 8;
-        if (row < ti.row_end && j < I) st_stream(P.act + row * I + j, v);
+        const uint32_t voff = j < I ? (uint32_t)(lane >> 2) * w.rowb + (uint32_t)j * 2u : kOOB;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) win_store(w, voff, q * 16, staged_chunk(stage, wave, q * 16 + (lane >> 2), c4));
       }
     } else if constexpr (KIND == KIND_NNS) {
       // fc2 dgrad: the tile is dact (bf16, as the reference stores it) for
       // columns j < I; with the forward's gate/up of the same rows it becomes
       // [d_gate | d_up] of dG1.  The round's gate/up loads go out first, so
       // that their latency overlaps the staging.
+      // gate/up (gin) and [d_gate | d_up] (c0) share one row layout.
       const int64_t I = P.I;
       const int cc = lane & 7;
       const int64_t j = (int64_t)ti.ntile * BN + wn * WCOLS + cc * 8;
+      const OutWin wi = out_window(P.gin, ti.row0 + rb, ti.row_end, 2 * I);
+      const OutWin wo = out_window(P.c0, ti.row0 + rb, ti.row_end, 2 * I);
+      const uint32_t vg = j < I ? (uint32_t)(lane >> 3) * wi.rowb + (uint32_t)j * 2u : kOOB;
+      const uint32_t vu = vg + (uint32_t)I * 2u;
       uint4 gv[8], uv[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int64_t row = ti.row0 + rb + q * 8 + (lane >> 3);
-        if (row < ti.row_end && j < I) {
-          gv[q] = ld_stream(P.gin + row * 2 * I + j);
-          uv[q] = ld_stream(P.gin + row * 2 * I + I + j);
-        } else {
-          gv[q] = uv[q] = make_uint4(0u, 0u, 0u, 0u);
-        }
+        gv[q] = win_load(wi, vg, q * 8);
+        uv[q] = win_load(wi, vu, q * 8);
       }
-      stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc4(acc[mt][nt], i); });
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int rl = q * 8 + (lane >> 3);
-        const int64_t row = ti.row0 + rb + rl;
-        const uint4 v = staged_chunk(stage, wave, rl, cc);
-        if (row < ti.row_end && j < I) {
-          float d[8], g[8], u[8], dg[8], du[8];
-          unpack8(v, d);
-          unpack8(gv[q], g);
-          unpack8(uv[q], u);
-          swiglu_bwd8(d, g, u, dg, du);
-          st_stream(P.c0 + row * 2 * I + j, pack8(dg));
-          st_stream(P.c0 + row * 2 * I + I + j, pack8(du));
-        }
+        const uint4 v = staged_chunk(stage, wave, q * 8 + (lane >> 3), cc);
+        float d[8], g[8], u[8], dg[8], du[8];
+        unpack8(v, d);
+        unpack8(gv[q], g);
+        unpack8(uv[q], u);
+        swiglu_bwd8(d, g, u, dg, du);
+        win_store(wo, vg, q * 8, pack8(dg));
+        win_store(wo, vu, q * 8, pack8(du));
       }
     } else if constexpr (KIND == KIND_TN) {
-      stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc4(acc[mt][nt], i); });
       const int cc = lane & 7;  // 16-byte chunk (8 columns) of the wave's 64
       const int64_t col = (int64_t)ti.ntile * BN + wn * WCOLS + cc * 8;
 #pragma unroll
@@ -619,25 +650,42 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
     } else {
       const int cc = lane & 7;  // 16-byte chunk (8 columns) of the wave's 64
       const int64_t col = (int64_t)ti.ntile * BN + wn * WCOLS + cc * 8;
-      stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc[mt][nt][i]; });
+      stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc4(acc[mt][nt], i); });
+      const OutWin w = out_window(P.c0, ti.row0 + rb, ti.row_end, P.ldc);
+      const uint32_t voff = col < P.N ? (uint32_t)(lane >> 3) * w.rowb + (uint32_t)col * 2u : kOOB;
+      // Mapped rows go to row dst of the whole output (dst is -1 for rows
+      // past the tile's group): through one descriptor over the output when
+      // it spans at most 2 GiB, else through 64-bit addresses.
+      const bool whole = (uint64_t)P.M * (uint64_t)P.ldc * 2u <= 0x7fffffffull;
+      const OutWin wd = {make_rsrc(KIND == KIND_NT ? P.cout : P.c0, (uint64_t)P.M * P.ldc * 2), w.rowb};
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const int rl = q * 8 + (lane >> 3);
-        const uint4 v = staged_chunk(stage, wave, rl, cc);
-        const int64_t row = ti.row0 + rb + rl;
-        if (row < ti.row_end && col < P.N) {
-          const int32_t d = dst[half * 8 + q];
-          if (KIND == KIND_NN && mapped) {
-            if ((uint32_t)d < (uint32_t)P.M) st_stream(P.c0 + (int64_t)d * P.ldc + col, v);
+        const uint4 v = staged_chunk(stage, wave, q * 8 + (lane >> 3), cc);
+        if (!(KIND == KIND_NN && mapped)) win_store(w, voff, q * 8, v);
+        const int32_t d = dst[half * 8 + q];
+        if ((KIND == KIND_NT || KIND == KIND_NN) && mapped && whole) {
+          const uint32_t vd = col < P.N && (uint32_t)d < (uint32_t)P.M ? (uint32_t)d * wd.rowb + (uint32_t)col * 2u : kOOB;
+          if (KIND == KIND_NN) {
+            win_store(wd, vd, 0, v);
           } else {
-            st_stream(P.c0 + row * P.ldc + col, v);
-          }
-          if (KIND == KIND_NT && mapped && (uint32_t)d < (uint32_t)P.M) {
-            // the weighted combine of a top-1 row, as the combine kernel rounds it
             float f[8];
             unpack8(v, f);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) f[j] = 0.f + round_bf16(f[j] * wt[half * 8 + q]);
+            for (int j = 0; j < 8; ++j) f[j] = __builtin_fmaf(f[j], wt[half * 8 + q], 0.f);
+            win_store(wd, vd, 0, pack8(f));
+          }
+        } else if ((KIND == KIND_NT || KIND == KIND_NN) && mapped && col < P.N && (uint32_t)d < (uint32_t)P.M) {
+          if (KIND == KIND_NN) {
+            st_stream(P.c0 + (int64_t)d * P.ldc + col, v);
+          } else {
+            // The weighted combine of a top-1 row, as the combine kernel
+            // rounds it: 0 + bf16(f * w).  The fma's single rounding of
+            // f * w + 0 is the product's, with -0 made +0, and pack8 rounds
+            // it to bf16.
+            float f[8];
+            unpack8(v, f);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) f[j] = __builtin_fmaf(f[j], wt[half * 8 + q], 0.f);
             st_stream(P.cout + (int64_t)d * P.ldc + col, pack8(f));
           }
         }
@@ -1180,8 +1228,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   // k-step KS of the current K-tile: MFMAs of k-step KS-1 (fragments `fm`)
   // interleaved with the reads of k-step KS into `fr`, and, with LOADS, the
   // loads of the next K-tile that fall into this k-step's groups (RS: the
-  // pieces that fall into them).
-  auto kstep = [&](auto ks, auto loads, auto oper, const char* stage, char* refill, const Frags<BM>& fm,
+  // pieces that fall into them).  FIRST: k-step KS-1 is the tile's first.
+  auto kstep = [&](auto ks, auto loads, auto first, const char* stage, char* refill, const Frags<BM>& fm,
                    Frags<BM>& fr) __attribute__((always_inline)) {
     static_for<0, NF>([&](auto jj) __attribute__((always_inline)) {
       constexpr int j = decltype(jj)::value;
@@ -1198,7 +1246,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
         });
       }
       reads_half(jj, stage, ks, fr);
-      mma_some<BM, j * PER, PER>(fm, acc);
+      mma_some<BM, j * PER, PER, decltype(first)::value>(fm, acc);
       __builtin_amdgcn_sched_barrier(0);
     });
   };
@@ -1206,7 +1254,6 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   for (;;) {
     // Output tile `cur`: its first K-tile is in stage cs, and the next stream
     // K-tile is in flight into the other stage.
-    zero_acc<BM>(acc);
     {
       // K-tile 0: no MFMAs pending, and the next K-tile is already in flight.
       const char* stage = lds + cs * STAGE_BYTES;
@@ -1221,7 +1268,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
         constexpr int j = decltype(jj)::value;
         read_frag<KIND, BM, frag_order(j)>(stage, 0, wm, wn, lane, f0);
       });
-      kstep(Int<1>{}, Int<0>{}, Int<0>{}, stage, refill, f0, f1);
+      kstep(Int<1>{}, Int<0>{}, Int<1>{}, stage, refill, f0, f1);
       kstep(Int<2>{}, Int<0>{}, Int<0>{}, stage, refill, f1, f0);
       kstep(Int<3>{}, Int<0>{}, Int<0>{}, stage, refill, f0, f1);
       if constexpr (RS) {

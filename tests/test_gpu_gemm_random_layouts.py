@@ -97,3 +97,30 @@ def test_random_shapes_every_kind(cuda, seed):
         assert torch.equal(c2, y) and torch.equal(out, ref_out), f"{name}: fc2 + combine differs from fc2, combine"
         dxp = kernels.group_gemm_nn_unpermute_top1(dy, w2, offd, perm)
         assert torch.equal(dxp[perm.long()], dact), f"{name}: dgrad + unpermute differs from dgrad, unpermute"
+
+
+def test_top1_outputs_past_2gib(cuda):
+    """Top-1 outputs of more than 2 GiB (rows past the 32-bit byte offsets of
+    one buffer descriptor) take the 64-bit store path; they must still equal
+    the plain GEMM followed by the separate row operation bit for bit."""
+    A, K, N = 131200, 64, 8192  # A * N * 2 bytes > 2^31
+    off = np.array([0, 70000, A], dtype=np.int64)
+    offd = torch.as_tensor(off, dtype=torch.int32, device=cuda)
+    gen = torch.Generator(device=cuda).manual_seed(77)
+    print(f"top-1 > 2 GiB: A={A} K={K} N={N}", flush=True)
+    act = torch.randn((A, K), generator=gen, device=cuda).to(torch.bfloat16)
+    w2 = (torch.randn((2, N, K), generator=gen, device=cuda) * 0.1).to(torch.bfloat16)
+    perm = torch.randperm(A, generator=gen, device=cuda).to(torch.int32)
+    rw = (0.05 + 0.95 * torch.rand((A,), generator=gen, device=cuda)).to(torch.bfloat16)
+    y = kernels.group_gemm_nt(act, w2, offd)
+    c2, out = kernels.group_gemm_nt_combine_top1(act, w2, offd, perm, rw)
+    assert torch.equal(c2, y)
+    ref_out = torch.empty_like(out)
+    ref_out[perm.long()] = (y * rw[:, None]).float().add_(0.0).to(torch.bfloat16)
+    assert torch.equal(out, ref_out), "fc2 + combine past 2 GiB differs from fc2, combine"
+    del c2, out, ref_out
+    b = w2.transpose(1, 2).contiguous()  # [2, K, N]
+    dy = act
+    dact = kernels.group_gemm_nn(dy, b, offd)
+    dxp = kernels.group_gemm_nn_unpermute_top1(dy, b, offd, perm)
+    assert torch.equal(dxp[perm.long()], dact), "dgrad + unpermute past 2 GiB differs from dgrad, unpermute"
