@@ -55,7 +55,8 @@ constexpr int NWAVES = 8, WAVES_N = 4;
 constexpr int NTHREADS = 64 * NWAVES;
 constexpr int WROWS = 128, WCOLS = 64;  // output tile of one wave
 constexpr int MT = WROWS / 32, NTT = WCOLS / 32;
-constexpr int kMaxGroups = 2048;
+constexpr int kMaxGroups = 2048;  // group ids fit 12 bits
+constexpr int kTileTab = 1024;    // decoded tiles per block kept in LDS (ragged-M kinds)
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always fails the range check
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
@@ -850,9 +851,12 @@ __device__ __forceinline__ void band_order(int64_t t, int64_t mtiles, int64_t nt
 // prefix `tpre`, ntn n-tiles each); TN walks the tiles_per_group weight tiles
 // of each group, whose K is the group's row count.  `local` >= 0 (TN only)
 // names tile `local` of group `tile` instead of a position in the list.
-template <int KIND, int BM>
+// UNI: `tile` is uniform over the wave and the result is made so; else each
+// lane decodes its own tile (the block's tile table, filled at kernel start).
+template <int KIND, int BM, bool UNI = true>
 __device__ __forceinline__ TileInfo decode_tile(const GemmParams& P, int64_t tile, const int32_t* tpre, int G,
                                                 int64_t ntn, int64_t tiles_per_group, int64_t local = -1) {
+  auto rd = [](int32_t v) { return UNI ? uni(v) : v; };
   TileInfo ti;
   int64_t m, n;
   if constexpr (KIND == KIND_TN) {
@@ -873,22 +877,22 @@ __device__ __forceinline__ TileInfo decode_tile(const GemmParams& P, int64_t til
     int lo = 0, hi = G;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
-      if (uni(tpre[mid]) <= m) lo = mid;
+      if (rd(tpre[mid]) <= m) lo = mid;
       else hi = mid - 1;
     }
     ti.g = lo;
-    ti.mtile = (int32_t)m - uni(tpre[lo]);
+    ti.mtile = (int32_t)m - rd(tpre[lo]);
     ti.row0 = P.offsets[lo] + ti.mtile * BM;
     ti.row_end = P.offsets[lo + 1];
     ti.nk = (int32_t)((P.K + BK - 1) / BK);
   }
   ti.ntile = (int32_t)n;
-  ti.g = uni(ti.g);
-  ti.mtile = uni(ti.mtile);
-  ti.ntile = uni(ti.ntile);
-  ti.row0 = uni(ti.row0);
-  ti.row_end = uni(ti.row_end);
-  ti.nk = uni(ti.nk);
+  ti.g = rd(ti.g);
+  ti.mtile = rd(ti.mtile);
+  ti.ntile = rd(ti.ntile);
+  ti.row0 = rd(ti.row0);
+  ti.row_end = rd(ti.row_end);
+  ti.nk = rd(ti.nk);
   return ti;
 }
 
@@ -1043,6 +1047,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE_BYTES];
   __shared__ int32_t tpre[kMaxGroups + 1];
   __shared__ int32_t scan_buf[NTHREADS];
+  __shared__ int4 ttab[KIND == KIND_TN ? 1 : kTileTab];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = uni(t >> 6);
@@ -1102,6 +1107,23 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   int64_t slot = blockIdx.x;
   if ((grid & 7) == 0) slot = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
 
+  // Ragged-M kinds: the block's first kTileTab tiles, decoded at once by its
+  // threads into LDS (entry s: tile slot + s * grid), so that moving on to the
+  // next tile costs one LDS read instead of a chain of dependent divisions,
+  // LDS reads and offset loads.
+  int32_t ntab = 0;
+  int32_t nk_all = 0;
+  if constexpr (KIND != KIND_TN) {
+    const int64_t mine = slot < total ? (total - slot + grid - 1) / grid : 0;
+    ntab = (int32_t)(mine < kTileTab ? mine : kTileTab);
+    nk_all = (int32_t)((P.K + BK - 1) / BK);
+    for (int e = t; e < ntab; e += NTHREADS) {
+      const TileInfo d = decode_tile<KIND, BM, false>(P, slot + (int64_t)e * grid, tpre, G, ntn, tiles_per_group);
+      ttab[e] = make_int4(d.row0, d.row_end, d.g | (d.ntile << 12), d.mtile);
+    }
+    __syncthreads();
+  }
+
   // The block's seq-th output tile; false past its last.  Plain order: tiles
   // slot, slot + grid, ...  Balanced wgrad order (BAL, grid = 8 XCDs x 32
   // blocks): copies by rank; in round seq, this block's XCD takes band
@@ -1112,6 +1134,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     if constexpr (!BAL) {
       const int64_t tile = slot + seq * grid;
       if (tile >= total) return false;
+      if (KIND != KIND_TN && seq < ntab) {
+        const int4 e = ttab[seq];
+        ti.row0 = uni(e.x);
+        ti.row_end = uni(e.y);
+        ti.g = uni(e.z) & 0xfff;
+        ti.ntile = uni(e.z) >> 12;
+        ti.mtile = uni(e.w);
+        ti.nk = nk_all;
+        return true;
+      }
       ti = decode_tile<KIND, BM>(P, tile, tpre, G, ntn, tiles_per_group);
       return true;
     } else {
