@@ -55,8 +55,10 @@ constexpr int NWAVES = 8, WAVES_N = 4;
 constexpr int NTHREADS = 64 * NWAVES;
 constexpr int WROWS = 128, WCOLS = 64;  // output tile of one wave
 constexpr int MT = WROWS / 32, NTT = WCOLS / 32;
-constexpr int kMaxGroups = 2048;  // group ids fit 12 bits
-constexpr int kTileTab = 1024;    // decoded tiles per block kept in LDS (ragged-M kinds)
+constexpr int kMaxGroups = 2048;
+constexpr int kTileTab = 1024;  // decoded tiles per block kept in LDS (ragged-M kinds)
+// A table entry packs the group id in 12 bits and the n-tile above it.
+static_assert(kMaxGroups <= (1 << 12), "group ids must fit the tile table's 12 bits");
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always fails the range check
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
@@ -1395,6 +1397,9 @@ int launch(const GemmParams& P, hipStream_t stream) {
       grouped_gemm_kernel<KIND_TN, kBM><<<grid, NTHREADS, 0, stream>>>(P);
     }
   } else {
+    // The LDS tile table keeps an n-tile index in 19 bits.
+    const int64_t ntn = KIND == KIND_FC1 ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
+    if (ntn >= (int64_t)1 << 19) return PMX_ERR_SHAPE;
     // FAST: K a multiple of 64, dgrad weights not split (P.b.split >= K).
     // RS (register-staged operands): fc1 and fc2 always; the fc1 dgrad when
     // the copies are small (under 8 m-tiles of rows on average), where each
