@@ -15,9 +15,10 @@
 // v_mfma_f32_32x32x16_bf16 with fp32 accumulators: while one wave of a SIMD
 // waits for LDS, a load or the barrier, the other keeps the matrix core busy.
 //
-// Operands stream HBM -> LDS with buffer_load ... lds (no VGPR staging)
-// through two 64 KB stages: K-tile p+1 lands in one stage while K-tile p is
-// multiplied from the other.  64-deep K-tiles make every row segment a load
+// Operands stream HBM -> LDS through two 64 KB stages, either with
+// buffer_load ... lds (no VGPR staging) or, in the register-staged variant,
+// through one VGPR per 1 KB piece: K-tile p+1 lands in one stage while
+// K-tile p is multiplied from the other.  64-deep K-tiles make every row segment a load
 // instruction fetches one whole 128-byte line.  A block walks its tiles as one
 // stream of K-tiles, so the next tile's first loads overlap the current
 // tile's end and epilogue.  The loads are issued as inline asm, one every
@@ -44,8 +45,9 @@ namespace {
 // segment is half a line, the L1 issues twice the requests to L2 for the
 // same bytes and the texture unit backs up behind it.
 constexpr int BN = 256, BK = 64;
-// Two pipeline stages of (BM + BN) x 64 bf16 (64 KB each) next to the
-// per-wave epilogue regions and the group prefix in 160 KB of LDS.
+// Two pipeline stages of (BM + BN) x 64 bf16 (64 KB each) next to the group
+// prefix and the block's decoded tile table in 160 KB of LDS; the epilogue
+// stages its output in the stage just freed.
 constexpr int NSTAGE = 2;
 // Eight waves, two per SIMD, in a 2 x 4 arrangement: each owns 128 x 64 of
 // the output as 4 x 2 tiles of v_mfma_f32_32x32x16_bf16 (128 AGPRs), so that
