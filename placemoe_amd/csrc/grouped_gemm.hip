@@ -1051,7 +1051,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   __shared__ __attribute__((aligned(1024))) char lds[NSTAGE * STAGE_BYTES];
   __shared__ int32_t tpre[kMaxGroups + 1];
   __shared__ int32_t scan_buf[NTHREADS];
-  __shared__ int4 ttab[KIND == KIND_TN ? 1 : kTileTab];
+  __shared__ int4 ttab[kTileTab];
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = uni(t >> 6);
@@ -1111,43 +1111,57 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   int64_t slot = blockIdx.x;
   if ((grid & 7) == 0) slot = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
 
-  // Ragged-M kinds: the block's first kTileTab tiles, decoded at once by its
-  // threads into LDS (entry s: tile slot + s * grid), so that moving on to the
-  // next tile costs one LDS read instead of a chain of dependent divisions,
-  // LDS reads and offset loads.
-  int32_t ntab = 0;
-  int32_t nk_all = 0;
-  if constexpr (KIND != KIND_TN) {
-    const int64_t mine = slot < total ? (total - slot + grid - 1) / grid : 0;
-    ntab = (int32_t)(mine < kTileTab ? mine : kTileTab);
-    nk_all = (int32_t)((P.K + BK - 1) / BK);
-    for (int e = t; e < ntab; e += NTHREADS) {
-      const TileInfo d = decode_tile<KIND, BM, false>(P, slot + (int64_t)e * grid, tpre, G, ntn, tiles_per_group);
-      ttab[e] = make_int4(d.row0, d.row_end, d.g | (d.ntile << 12), d.mtile);
-    }
-    __syncthreads();
-  }
-
   // The block's seq-th output tile; false past its last.  Plain order: tiles
   // slot, slot + grid, ...  Balanced wgrad order (BAL, grid = 8 XCDs x 32
   // blocks): copies by rank; in round seq, this block's XCD takes band
   // 8 seq + deal[seq] (past the table: 8 seq + x, or 8 seq + 7 - x when seq
   // is odd) and its block j tile j of it.
   const unsigned char* deal = reinterpret_cast<const unsigned char*>(tpre + G);
+
+  // The block's first kTileTab tiles, decoded at once by its threads into LDS
+  // (entry s: the block's s-th tile; mtile -1 past its last), so that moving
+  // on to the next tile costs one LDS read instead of a chain of dependent
+  // divisions, LDS reads and offset loads.  A block has at most
+  // ceil(total / grid) tiles in either order.
+  const int64_t rounds = (total + grid - 1) / grid;
+  const int32_t ntab = (int32_t)(rounds < kTileTab ? rounds : kTileTab);
+  const int32_t nk_all = KIND == KIND_TN ? 0 : (int32_t)((P.K + BK - 1) / BK);
+  for (int e = t; e < ntab; e += NTHREADS) {
+    TileInfo d;
+    bool ok;
+    if constexpr (!BAL) {
+      const int64_t tile = slot + (int64_t)e * grid;
+      ok = tile < total;
+      if (ok) d = decode_tile<KIND, BM, false>(P, tile, tpre, G, ntn, tiles_per_group);
+    } else {
+      const int32_t x = e < deal_rounds ? (int32_t)deal[e] : ((e & 1) ? kNumXcd - 1 - xcd : xcd);
+      const int64_t tile = ((int64_t)e * kNumXcd + x) * kBandTiles + xj;
+      ok = tile < total;
+      if (ok) {
+        const int64_t rank = tile / tiles_per_group;
+        d = decode_tile<KIND, BM, false>(P, scan_buf[rank], tpre, G, ntn, tiles_per_group,
+                                         tile - rank * tiles_per_group);
+      }
+    }
+    ttab[e] = ok ? make_int4(d.row0, d.row_end, d.g | (d.ntile << 12), d.mtile) : make_int4(0, 0, 0, -1);
+  }
+  __syncthreads();
+
   auto tile_at = [&](int64_t seq, TileInfo& ti) -> bool {
+    if (seq < ntab) {
+      const int4 e = ttab[seq];
+      if (uni(e.w) < 0) return false;
+      ti.row0 = uni(e.x);
+      ti.row_end = uni(e.y);
+      ti.g = uni(e.z) & 0xfff;
+      ti.ntile = uni(e.z) >> 12;
+      ti.mtile = uni(e.w);
+      ti.nk = KIND == KIND_TN ? (int32_t)(((int64_t)ti.row_end - ti.row0 + BK - 1) / BK) : nk_all;
+      return true;
+    }
     if constexpr (!BAL) {
       const int64_t tile = slot + seq * grid;
       if (tile >= total) return false;
-      if (KIND != KIND_TN && seq < ntab) {
-        const int4 e = ttab[seq];
-        ti.row0 = uni(e.x);
-        ti.row_end = uni(e.y);
-        ti.g = uni(e.z) & 0xfff;
-        ti.ntile = uni(e.z) >> 12;
-        ti.mtile = uni(e.w);
-        ti.nk = nk_all;
-        return true;
-      }
       ti = decode_tile<KIND, BM>(P, tile, tpre, G, ntn, tiles_per_group);
       return true;
     } else {
@@ -1385,6 +1399,9 @@ template <int KIND>
 int launch(const GemmParams& P, hipStream_t stream) {
   const int grid = grid_size();
   if (grid <= 0) return PMX_ERR_HIP;
+  // The LDS tile table keeps an n-tile index in 19 bits.
+  const int64_t ntn = KIND == KIND_FC1 ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
+  if (ntn >= (int64_t)1 << 19) return PMX_ERR_SHAPE;
   if constexpr (KIND == KIND_TN) {
     // FAST: every row of both operands within 31-bit offsets (P.K = their rows).
     const bool fast = fits_rsrc(P.K, P.M) && fits_rsrc(P.K, P.N);
@@ -1399,9 +1416,6 @@ int launch(const GemmParams& P, hipStream_t stream) {
       grouped_gemm_kernel<KIND_TN, kBM><<<grid, NTHREADS, 0, stream>>>(P);
     }
   } else {
-    // The LDS tile table keeps an n-tile index in 19 bits.
-    const int64_t ntn = KIND == KIND_FC1 ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
-    if (ntn >= (int64_t)1 << 19) return PMX_ERR_SHAPE;
     // FAST: K a multiple of 64, dgrad weights not split (P.b.split >= K).
     // RS (register-staged operands): fc1 and fc2 always; the fc1 dgrad when
     // the copies are small (under 8 m-tiles of rows on average), where each
