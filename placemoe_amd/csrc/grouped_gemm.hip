@@ -1397,11 +1397,11 @@ constexpr int64_t kRsMaxRowsPerCopy = 8 * kBM;
 
 template <int KIND>
 int launch(const GemmParams& P, hipStream_t stream) {
-  const int grid = grid_size();
-  if (grid <= 0) return PMX_ERR_HIP;
   // The LDS tile table keeps an n-tile index in 19 bits.
   const int64_t ntn = KIND == KIND_FC1 ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
   if (ntn >= (int64_t)1 << 19) return PMX_ERR_SHAPE;
+  const int grid = grid_size();
+  if (grid <= 0) return PMX_ERR_HIP;
   if constexpr (KIND == KIND_TN) {
     // FAST: every row of both operands within 31-bit offsets (P.K = their rows).
     const bool fast = fits_rsrc(P.K, P.M) && fits_rsrc(P.K, P.N);

@@ -108,3 +108,14 @@ def test_wgrad_output_layout_rejected_before_any_launch():
     assert tn(p, p, p, G, K, M, N, p, p, (M // 2) * N, 0, None) == _capi.PMX_ERR_ARG
     assert tn(p, p, p, G, K, M, N, p, p, (M // 2) * N, M, None) == _capi.PMX_ERR_ARG
     assert tn(p, p, p, G, K, M, N, p, p, (M // 2) * N - 8, M // 2, None) == _capi.PMX_ERR_ARG
+
+
+def test_fc1_n_tiles_beyond_the_tile_table_rejected_before_any_launch():
+    """A tile's n-index is packed in 19 bits of the kernel's LDS tile table:
+    fc1 shapes with 2^19 or more 128-column n-tiles (I >= 2^26) are refused
+    on the host with PMX_ERR_SHAPE, before the device is touched."""
+    lib = _capi.load()
+    p = ctypes.c_void_p(256)
+    H, I = 8, 1 << 26
+    rc = lib.pmx_gemm_fc1_swiglu_fwd(p, p, p, 2 * I * H, p, 1, 256, H, I, p, p, None)
+    assert rc == _capi.PMX_ERR_SHAPE
