@@ -207,7 +207,6 @@ __device__ __forceinline__ void dma_kc(char* lds, const Operand& op, int32_t kt,
   const bool tail = kt == op.ktail;
   const __amdgpu_buffer_rsrc_t none = empty_rsrc(op.base);
   const __amdgpu_buffer_rsrc_t r0 = live ? op.r0 : none;
-  const __amdgpu_buffer_rsrc_t r1 = live ? op.r1 : none;
 #pragma unroll
   for (int q0 = Q0B; q0 < Q0E; ++q0) {
     const int q = q0 * NWAVES + wave;
