@@ -6,6 +6,7 @@ The library is loaded from ``placemoe_amd/_lib/``; a missing library raises
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
@@ -153,6 +154,19 @@ def load(path: os.PathLike | None = None) -> ctypes.CDLL:
     if path is None:
         _LIB = lib
     return lib
+
+
+@contextlib.contextmanager
+def using(path: os.PathLike):
+    """Route every call through another build of the same C ABI (a library
+    variant under test) until the block ends."""
+    global _LIB
+    prev = _LIB
+    _LIB = load(path)
+    try:
+        yield _LIB
+    finally:
+        _LIB = prev
 
 
 def error_string(code: int) -> str:

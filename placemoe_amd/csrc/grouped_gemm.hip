@@ -58,7 +58,14 @@ constexpr int NTHREADS = 64 * NWAVES;
 constexpr int WROWS = 128, WCOLS = 64;  // output tile of one wave
 constexpr int MT = WROWS / 32, NTT = WCOLS / 32;
 constexpr int kMaxGroups = 2048;
-constexpr int kTileTab = 1024;  // decoded tiles per block kept in LDS (ragged-M kinds)
+// Decoded tiles per block kept in LDS; a block's tiles past the table are
+// decoded on the spot.  PMX_TILE_TAB overrides it for a test build that runs
+// that path at small shapes.
+#ifndef PMX_TILE_TAB
+#define PMX_TILE_TAB 1024
+#endif
+constexpr int kTileTab = PMX_TILE_TAB;
+static_assert(kTileTab >= 1 && kTileTab <= 1024, "tile table: 1 .. 1024 entries (16 KB of LDS)");
 // A table entry packs the group id in 12 bits and the n-tile above it.
 static_assert(kMaxGroups <= (1 << 12), "group ids must fit the tile table's 12 bits");
 constexpr uint32_t kOOB = 0x80000000u;  // buffer offset that always fails the range check
@@ -228,8 +235,9 @@ __device__ __forceinline__ void dma_mn(char* lds, const Operand& op, int32_t kt,
   constexpr int ROWS = 1024 / (2 * W);
   if constexpr (FAST && REBASE) {
     // Weight gradient whose operands fit 31-bit offsets: one descriptor per
-    // group (rows past its end fail the range check), the K-tile advance in
-    // the scalar offset.
+    // group, the K-tile advance in the scalar offset; the range check covers
+    // vector plus scalar offset, so rows past the group's end load zeros
+    // (pinned by a GPU test with NaN rows past the last group).
     const uint32_t soff = (uint32_t)kt * (uint32_t)BK * op.ldb;
 #pragma unroll
     for (int q0 = Q0B; q0 < Q0E; ++q0) {
@@ -518,8 +526,9 @@ __device__ __forceinline__ uint4 staged_chunk(const char* stage, int wave, int r
 // that the range check drops the loads (zeros) and stores of rows past the
 // tile's group: no 64-bit address arithmetic and no branch per store.  The
 // whole offset, row and column, is the 32-bit vector offset (kOOB for columns
-// past the tensor): the range check covers the vector offset only, not the
-// scalar one.
+// past the tensor).  (The range check covers the sum of the vector and scalar
+// offsets, which the weight gradient's FAST loads rely on; the stores keep
+// the scalar offset at 0.)
 struct OutWin {
   __amdgpu_buffer_rsrc_t r;
   uint32_t rowb;  // bytes per row

@@ -25,9 +25,10 @@ import torch
 
 from . import kernels
 
-# Route checks whose status copy has not been looked at yet (forward-only
-# calls have no backward to look at them); each forward polls them without
-# waiting and raises for the first that reports an invalid id.
+# Route checks whose status copy has not been looked at yet.  The op never
+# waits for one: each forward and backward polls them (an event query) and
+# raises for the first that has landed and reports an invalid id; a check
+# whose copy is still in flight stays here for the next poll.
 _PENDING_CHECKS: list = []
 
 
@@ -35,6 +36,18 @@ def _sync_route_checks() -> bool:
     """PLACEMOE_AMD_CHECK_ROUTES=1: check every forward's routing on the spot
     (one stream synchronisation per call)."""
     return os.environ.get("PLACEMOE_AMD_CHECK_ROUTES", "0") not in ("", "0")
+
+
+def check_pending_routes(block: bool = False) -> None:
+    """Raise ``ValueError`` if a routing call whose status has landed flagged
+    an invalid expert or source id.  ``block=True`` first waits for every
+    pending status copy (a host synchronisation: for the end of a step or a
+    test); the default only looks at copies that have already landed."""
+    if block:
+        for check in _PENDING_CHECKS:
+            if not check.checked:
+                check.raise_if_failed()
+    _poll_pending_checks()
 
 
 # Backward GEMM pairs that do not depend on each other (fc2 dgrad and fc2
@@ -95,15 +108,22 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 
 
 def _poll_pending_checks() -> None:
+    """Look at every pending check whose copy has landed (no waiting); the
+    first that failed raises.  Checks still in flight are kept."""
     keep = []
+    failed = None
     for check in _PENDING_CHECKS:
         if check.checked:
             continue
         if check.ready():
-            check.raise_if_failed()
+            check.checked = True
+            if failed is None and check.failed():
+                failed = check
         else:
             keep.append(check)
-    _PENDING_CHECKS[:] = keep[-64:]
+    _PENDING_CHECKS[:] = keep
+    if failed is not None:
+        failed.raise_if_failed()
 
 
 class _ExpertLayerBase(torch.autograd.Function):
@@ -129,13 +149,13 @@ class _ExpertLayerBase(torch.autograd.Function):
         r = kernels.route(selected, C, mapping=mapping, sources=sources, source=source)
         # Invalid expert or source ids are clamped on the device and flagged in
         # the routing status word.  Its copy is checked without a host sync:
-        # at the start of the backward, or by a later forward.
+        # by the backward if it has landed by then, else by a later forward or
+        # backward (or check_pending_routes).
         check = kernels.RouteCheck(r)
         if _sync_route_checks():
             check.raise_if_failed()
         else:
             _PENDING_CHECKS.append(check)
-        ctx.route_check = check
         if recorder is not None:
             recorder(r.counts)
         row_src = None
@@ -157,7 +177,7 @@ class _ExpertLayerBase(torch.autograd.Function):
 
     @staticmethod
     def _backward(ctx, grad_out):
-        ctx.route_check.raise_if_failed()
+        _poll_pending_checks()
         xp, gu, act, y, pos, offsets, w, w_gate, w_up, fc2_weight, row_src = ctx.saved_tensors
         grad_out = grad_out.contiguous()
         need_w, need_x = ctx.needs_input_grad[1], ctx.needs_input_grad[0]

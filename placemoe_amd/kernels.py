@@ -114,8 +114,8 @@ def route_status(r: Routing) -> int:
 
 class RouteCheck:
     """The routing status word, copied to pinned host memory behind the
-    routing kernels on the same stream.  ``failed()`` waits only for that
-    copy, which the GPU finishes long before the host reaches the backward."""
+    routing kernels on the same stream.  ``ready()`` asks (without waiting)
+    whether the copy has landed; ``failed()`` waits for it."""
 
     def __init__(self, r: Routing):
         dev = r.workspace.device

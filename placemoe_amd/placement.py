@@ -295,6 +295,130 @@ class LayerPlacement:
     def clear_slot_tokens(self) -> None:
         self.accumulated_slot_tokens = None
 
+    @classmethod
+    def from_layer_state(cls, state, source_rank: int, key: str | None = None) -> "LayerStatePlacement":
+        """A placement that reads ``L`` and ``M`` from the reference's own
+        per-layer state on every call instead of keeping a copy (see
+        ``LayerStatePlacement``)."""
+        return LayerStatePlacement(state, source_rank, key=key)
+
+
+class LayerStatePlacement:
+    """Placement backed by the reference's ``ExpertLayerState``
+    (veomni/distributed/moe/hiermoe/expert_swap.py:433-586), read on every
+    call, so that the reference's controller stays the one owner of ``M``.
+
+    Each forward routes with ``state.source_mapping_for_device(device,
+    source_rank)`` (expert_swap.py:502-510), the device row of ``M`` the
+    reference's own EP path gathers from; a mapping-only hot update
+    (``_install_hot_update_mapping``, expert_swap.py:10920-10972) replaces
+    ``state.source_logical_to_physical`` and clears that cache, so the next
+    forward here sees the new ``M``.  A state without a source-rank LUT
+    routes with ``state.mapping_for_device(device)`` (the owner table, as the
+    reference does).  With per-token ``token_sources`` the whole ``[S, E]``
+    table goes to the device, cached per table object and placement version.
+
+    Duck-typed: the state needs ``key``, ``num_experts``,
+    ``logical_to_physical``, ``slot_to_logical`` (or None: one copy per
+    expert), ``source_logical_to_physical``, ``placement_version`` and the two
+    ``*_mapping_for_device`` methods.
+    """
+
+    def __init__(self, state, source_rank: int, key: str | None = None):
+        self.state = state
+        self.key = key if key is not None else str(state.key)
+        self.source_rank = int(source_rank)
+        self.source = 0  # row 0 of the one-row table handed to the routing kernels
+        self.token_sources: torch.Tensor | None = None
+        self.accumulated_slot_tokens: torch.Tensor | None = None
+        self._cache: dict = {}
+
+    @property
+    def num_experts(self) -> int:
+        return int(self.state.num_experts)
+
+    @property
+    def slot_to_logical(self) -> np.ndarray:
+        L = self.state.slot_to_logical
+        if L is None:
+            # no slot layout: slot logical_to_physical[e] holds expert e
+            owners = np.asarray(torch.as_tensor(self.state.logical_to_physical).cpu(), dtype=np.int64)
+            L = np.full(int(owners.max()) + 1 if owners.size else 0, EMPTY_EXPERT, dtype=np.int64)
+            L[owners] = np.arange(owners.size)
+            return L
+        return np.asarray(torch.as_tensor(L).cpu(), dtype=np.int64)
+
+    @property
+    def owner_slots(self) -> np.ndarray:
+        return np.asarray(torch.as_tensor(self.state.logical_to_physical).cpu(), dtype=np.int64)
+
+    @property
+    def source_logical_to_physical(self) -> np.ndarray | None:
+        M = self.state.source_logical_to_physical
+        return None if M is None else np.asarray(torch.as_tensor(M).cpu(), dtype=np.int64)
+
+    @property
+    def placement_version(self) -> int:
+        return int(self.state.placement_version)
+
+    @property
+    def num_slots(self) -> int:
+        return int(self.slot_to_logical.shape[0])
+
+    def mapping_for_device(self, device: torch.device) -> torch.Tensor:
+        """``[S, E]`` int64 ``M`` on ``device`` for the routing kernels: the
+        state's device row of this source rank as a one-row table, or the
+        whole table when per-token sources are set."""
+        M = self.state.source_logical_to_physical
+        if self.token_sources is not None:
+            if M is None:
+                raise RuntimeError(f"HierMoE layer {self.key} has no source-rank route LUT.")
+            key = ("M", device, id(M), self.placement_version)
+            if key not in self._cache:
+                self._cache = {k: v for k, v in self._cache.items() if k[0] != "M"}
+                self._cache[key] = torch.as_tensor(M, dtype=torch.int64).to(device)
+            return self._cache[key]
+        if M is None:
+            row = self.state.mapping_for_device(device)
+        else:
+            row = self.state.source_mapping_for_device(device, self.source_rank)
+        return row.reshape(1, -1)
+
+    def copy_tables_for_device(self, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+        L = self.slot_to_logical
+        key = ("copies", device, L.tobytes())
+        if key not in self._cache:
+            self._cache = {k: v for k, v in self._cache.items() if k[0] != "copies"}
+            off, slots = copy_table(L, self.num_experts)
+            self._cache[key] = (torch.as_tensor(off).to(device), torch.as_tensor(slots).to(device))
+        return self._cache[key]
+
+    def install_mapping(self, source_logical_to_physical) -> int:
+        """Mapping-only hot update written into the state the way the
+        reference's ``_install_hot_update_mapping`` writes it
+        (expert_swap.py:10963-10972); returns 1 if ``M`` changed."""
+        lut = torch.as_tensor(np.asarray(source_logical_to_physical, dtype=np.int64))
+        M = self.state.source_logical_to_physical
+        if M is not None and tuple(lut.shape) != tuple(M.shape):
+            raise RuntimeError(f"PlaceMoE mapping for {self.key} has shape {tuple(lut.shape)}, "
+                               f"expected {tuple(M.shape)}.")
+        L = self.slot_to_logical
+        if bool(((lut < 0) | (lut >= L.shape[0])).any()):
+            raise RuntimeError(f"PlaceMoE mapping for {self.key} references an invalid slot.")
+        if not np.array_equal(L[lut.numpy()], np.broadcast_to(np.arange(self.num_experts), tuple(lut.shape))):
+            raise RuntimeError(f"PlaceMoE mapping for {self.key} references the wrong expert.")
+        changed = M is None or not torch.equal(torch.as_tensor(M).cpu(), lut)
+        self.state.source_logical_to_physical = lut.clone()
+        self.state._device_source_mapping_cache.clear()
+        self.state.placement_version += int(changed)
+        return int(changed)
+
+    def record_slot_tokens(self, counts: torch.Tensor) -> None:
+        LayerPlacement.record_slot_tokens(self, counts)
+
+    def clear_slot_tokens(self) -> None:
+        self.accumulated_slot_tokens = None
+
 
 class PlacementRegistry:
     """layer_key -> LayerPlacement, plus parameter -> layer_key lookup (the
@@ -304,13 +428,13 @@ class PlacementRegistry:
         self.layers: dict[str, LayerPlacement] = {}
         self._param_keys: dict[int, str] = {}
 
-    def register(self, placement: LayerPlacement, *params: torch.Tensor) -> None:
+    def register(self, placement: "LayerPlacement | LayerStatePlacement", *params: torch.Tensor) -> None:
         self.layers[placement.key] = placement
         for p in params:
             if p is not None:
                 self._param_keys[id(p)] = placement.key
 
-    def get(self, key: str | None) -> LayerPlacement | None:
+    def get(self, key: str | None) -> "LayerPlacement | LayerStatePlacement | None":
         return None if key is None else self.layers.get(key)
 
     def key_from_params(self, *params: torch.Tensor | None) -> str | None:

@@ -29,7 +29,7 @@ from typing import Sequence
 import numpy as np
 import torch
 
-from . import _capi, kernels
+from . import _capi, experts, kernels
 from .placement import PLACEMENTS, LayerPlacement
 
 
@@ -134,7 +134,10 @@ class OverlappedReplicaSync:
     def finish(self) -> dict[str, tuple[torch.Tensor, torch.Tensor]]:
         """The caller's stream waits for every enqueued fold; returns the fp32
         logical gradients of the layers folded since the last call and clears
-        their accumulated token counts."""
+        their accumulated token counts.  Routing checks of the step whose
+        status has landed are looked at (no waiting): an invalid expert id
+        raises ``ValueError`` here at the latest."""
+        experts.check_pending_routes()
         for device, side in self._streams.items():
             main = torch.cuda.current_stream(device)
             main.wait_stream(side)

@@ -1,7 +1,7 @@
 """Floating-point parity at the full benchmark shapes, stage by stage.
 
 Every kernel of the layer runs at the full shape of a benchmark config
-(config 2: T=16384, K=8, H=2048, I=768, 160 copies; config 3: 65536 rows over
+(config 1: T=4096, K=2, H=1024, I=2816, 12 copies of 8 experts; config 2: T=16384, K=8, H=2048, I=768, 160 copies; config 3: 65536 rows over
 16 copies of 1.2k-19.4k rows, H=7168, I=2048; config 4: T=32768, K=4, H=4096,
 I=1536, 96 copies with empty and tiny ones; config 5: the config-2 shape over
 256 copies of 128 experts).  Each
@@ -78,7 +78,8 @@ def _check_wgrad(name, grad, a, b, offsets, groups, rng, tiles_per_group=4):
 
 
 @pytest.mark.parametrize("config,per_group,tokens_checked",
-                         [("qwen3", 24, 2048), ("dsv3", 256, 2048), ("skew", 48, 2048), ("fold", 16, 2048)])
+                         [("toy", 64, 4096), ("qwen3", 24, 2048), ("dsv3", 256, 2048), ("skew", 48, 2048),
+                          ("fold", 16, 2048)])
 def test_full_shape_stagewise(cuda, config, per_group, tokens_checked):
     torch.set_num_threads(min(16, torch.get_num_threads()))
     wl = make_workload(config, device=cuda)
@@ -113,6 +114,26 @@ def test_full_shape_stagewise(cuda, config, per_group, tokens_checked):
     dx = kernels.moe_gather(dxp, r.pos)
     torch.cuda.synchronize()
     print(f"kernels done; copy rows min {counts.min()} max {counts.max()} empty {(counts == 0).sum()}", flush=True)
+
+    if K == 1:
+        # The top-1 entry points the layer (and bench.py) runs instead: the
+        # permute that records each row's token and weight, fc2 with the
+        # combine in its epilogue and the fc1 dgrad with the unpermute
+        # gradient in its epilogue.  Bit for bit against the unfused kernels
+        # above, at this shape.
+        xp1, row_src, row_w = kernels.moe_scatter_src(wl.hidden, r.pos, w)
+        y1, out1 = kernels.group_gemm_nt_combine_top1(act, wl.fc2, r.offsets, row_src, row_w)
+        dx1 = kernels.group_gemm_nn_unpermute_top1(dg1, wl.fc1, r.offsets, row_src)
+        torch.cuda.synchronize()
+        assert torch.equal(xp1, xp), "moe_scatter_src rows differ from moe_scatter"
+        rows = r.pos.reshape(-1).long()
+        assert torch.equal(row_src[rows].long(), torch.arange(T, device=cuda)), "row_src is not the row's token"
+        assert torch.equal(row_w[rows], w.reshape(-1)), "row_w is not the row's router weight"
+        assert torch.equal(y1, y), "fc2 + combine: Y differs from group_gemm_nt"
+        assert torch.equal(out1, out), "fc2 + combine: output differs from combine_fwd"
+        assert torch.equal(dx1, dx), "fc1 dgrad + unpermute differs from group_gemm_nn + moe_gather"
+        del xp1, y1, out1, dx1
+        print("top-1 fused entry points bit-identical at full shape", flush=True)
 
     # --- row-sampled GEMM stages, each fed its own GPU inputs
     w1c, w2c = wl.fc1.cpu(), wl.fc2.cpu()
@@ -154,3 +175,20 @@ def test_full_shape_stagewise(cuda, config, per_group, tokens_checked):
     dxp_s = dxp[torch.as_tensor(pos_s.reshape(-1), device=cuda).long()].cpu()
     assert_bf16_close(dx[tt].cpu(), O.unpermute_grad(dxp_s, local), name="unpermute grad")
     print("row kernels ok", flush=True)
+
+
+def test_toy_config_full_forward_matches_oracle(cuda):
+    """Config 1, the CPU-runnable case, at its full 4096 tokens: the layer's
+    forward (the configuration is forward-only) against the oracle's."""
+    from placemoe_amd import experts
+
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    wl = make_workload("toy")
+    assert wl.T == 4096 and wl.K == 2 and wl.C == 12
+    with torch.no_grad():
+        out = experts.expert_layer(wl.hidden.to(cuda), wl.routing_weights.to(cuda), wl.selected.to(cuda),
+                                   wl.fc2.to(cuda), fc1_1_2_weight=wl.fc1.to(cuda), mapping=wl.mapping.to(cuda),
+                                   sources=wl.sources.to(cuda))
+    phys = O.map_logical_to_physical(wl.mapping.numpy(), wl.sources.numpy(), wl.selected.numpy())
+    fwd = O.moe_layer_forward(wl.hidden, wl.routing_weights, phys, wl.fc1, wl.fc2)
+    assert_bf16_close(out, fwd["out"], name="config-1 layer output")

@@ -49,6 +49,50 @@ def _per_group(a, off, fn):
     return out
 
 
+def check_every_kind(cuda, off, H, I, gen_seed, name):
+    """Every GEMM kind over the copies ``off`` (row offsets) against fp32
+    products on the GPU; the top-1 entry points bit for bit against the plain
+    GEMM plus the separate row operation."""
+    G = len(off) - 1
+    A = int(off[-1])
+    offd = torch.as_tensor(off, dtype=torch.int32, device=cuda)
+    gen = torch.Generator(device=cuda).manual_seed(gen_seed)
+
+    def rn(*shape, scale=1.0):
+        return (torch.randn(shape, generator=gen, device=cuda) * scale).to(torch.bfloat16)
+
+    x, dy = rn(A, H), rn(A, H)
+    w1, w2 = rn(G, 2 * I, H, scale=0.05), rn(G, H, I, scale=0.05)
+
+    gu, act = kernels.gemm_fc1_swiglu(x, w1, w1.view(-1)[I * H:], 2 * I * H, offd, G, I)
+    assert_bf16_close(gu, _per_group(x, off, lambda g, a: a @ w1[g].float().t()), name=f"{name} fc1")
+    y = kernels.group_gemm_nt(act, w2, offd)
+    assert_bf16_close(y, _per_group(act, off, lambda g, a: a @ w2[g].float().t()), name=f"{name} fc2")
+    dact = kernels.group_gemm_nn(dy, w2, offd)
+    ref_dact = _per_group(dy, off, lambda g, a: a @ w2[g].float())
+    assert_bf16_close(dact, ref_dact, name=f"{name} dgrad")
+    dg1 = kernels.gemm_fc2_dgrad_swiglu(dy, w2, gu, offd)
+    d = ref_dact.to(torch.bfloat16).float()
+    gate, up = gu[:, :I].float(), gu[:, I:].float()
+    sg = torch.sigmoid(gate)
+    assert_bf16_close(dg1[:, :I], d * up * sg * (1 + gate * (1 - sg)), name=f"{name} d_gate")
+    assert_bf16_close(dg1[:, I:], d * (gate * sg).to(torch.bfloat16).float(), name=f"{name} d_up")
+    wg = kernels.group_gemm_tn(dy, act, offd)
+    for g in range(G):
+        s, e = int(off[g]), int(off[g + 1])
+        ref = dy[s:e].float().t() @ act[s:e].float() if e > s else torch.zeros((H, I), device=cuda)
+        assert_bf16_close(wg[g], ref, name=f"{name} wgrad copy {g}")
+
+    perm = torch.randperm(A, generator=gen, device=cuda).to(torch.int32)
+    rw = (0.05 + 0.95 * torch.rand((A,), generator=gen, device=cuda)).to(torch.bfloat16)
+    c2, out = kernels.group_gemm_nt_combine_top1(act, w2, offd, perm, rw)
+    ref_out = torch.empty_like(out)
+    ref_out[perm.long()] = ((y.float() * rw.float()[:, None]).to(torch.bfloat16).float() + 0.0).to(torch.bfloat16)
+    assert torch.equal(c2, y) and torch.equal(out, ref_out), f"{name}: fc2 + combine differs from fc2, combine"
+    dxp = kernels.group_gemm_nn_unpermute_top1(dy, w2, offd, perm)
+    assert torch.equal(dxp[perm.long()], dact), f"{name}: dgrad + unpermute differs from dgrad, unpermute"
+
+
 @pytest.mark.parametrize("seed", [101, 202, 303, 404])
 def test_random_shapes_every_kind(cuda, seed):
     rng = np.random.default_rng(seed)
@@ -60,43 +104,7 @@ def test_random_shapes_every_kind(cuda, seed):
         print(f"seed {seed} case {case}: G={G} A={A} H={H} I={I}", flush=True)
         if A == 0:
             continue
-        offd = torch.as_tensor(off, dtype=torch.int32, device=cuda)
-        gen = torch.Generator(device=cuda).manual_seed(seed * 1000 + case)
-
-        def rn(*shape, scale=1.0):
-            return (torch.randn(shape, generator=gen, device=cuda) * scale).to(torch.bfloat16)
-
-        x, dy = rn(A, H), rn(A, H)
-        w1, w2 = rn(G, 2 * I, H, scale=0.05), rn(G, H, I, scale=0.05)
-        name = f"seed {seed} case {case}"
-
-        gu, act = kernels.gemm_fc1_swiglu(x, w1, w1.view(-1)[I * H:], 2 * I * H, offd, G, I)
-        assert_bf16_close(gu, _per_group(x, off, lambda g, a: a @ w1[g].float().t()), name=f"{name} fc1")
-        y = kernels.group_gemm_nt(act, w2, offd)
-        assert_bf16_close(y, _per_group(act, off, lambda g, a: a @ w2[g].float().t()), name=f"{name} fc2")
-        dact = kernels.group_gemm_nn(dy, w2, offd)
-        ref_dact = _per_group(dy, off, lambda g, a: a @ w2[g].float())
-        assert_bf16_close(dact, ref_dact, name=f"{name} dgrad")
-        dg1 = kernels.gemm_fc2_dgrad_swiglu(dy, w2, gu, offd)
-        d = ref_dact.to(torch.bfloat16).float()
-        gate, up = gu[:, :I].float(), gu[:, I:].float()
-        sg = torch.sigmoid(gate)
-        assert_bf16_close(dg1[:, :I], d * up * sg * (1 + gate * (1 - sg)), name=f"{name} d_gate")
-        assert_bf16_close(dg1[:, I:], d * (gate * sg).to(torch.bfloat16).float(), name=f"{name} d_up")
-        wg = kernels.group_gemm_tn(dy, act, offd)
-        for g in range(G):
-            s, e = int(off[g]), int(off[g + 1])
-            ref = dy[s:e].float().t() @ act[s:e].float() if e > s else torch.zeros((H, I), device=cuda)
-            assert_bf16_close(wg[g], ref, name=f"{name} wgrad copy {g}")
-
-        perm = torch.randperm(A, generator=gen, device=cuda).to(torch.int32)
-        rw = (0.05 + 0.95 * torch.rand((A,), generator=gen, device=cuda)).to(torch.bfloat16)
-        c2, out = kernels.group_gemm_nt_combine_top1(act, w2, offd, perm, rw)
-        ref_out = torch.empty_like(out)
-        ref_out[perm.long()] = ((y.float() * rw.float()[:, None]).to(torch.bfloat16).float() + 0.0).to(torch.bfloat16)
-        assert torch.equal(c2, y) and torch.equal(out, ref_out), f"{name}: fc2 + combine differs from fc2, combine"
-        dxp = kernels.group_gemm_nn_unpermute_top1(dy, w2, offd, perm)
-        assert torch.equal(dxp[perm.long()], dact), f"{name}: dgrad + unpermute differs from dgrad, unpermute"
+        check_every_kind(cuda, off, H, I, seed * 1000 + case, f"seed {seed} case {case}")
 
 
 def test_top1_outputs_past_2gib(cuda):

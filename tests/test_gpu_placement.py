@@ -66,6 +66,52 @@ def test_mapping_hot_update_reaches_device_routing(cuda):
         PLACEMENTS.clear()
 
 
+@pytest.mark.parametrize("per_token", [False, True], ids=["source_rank_row", "per_token_sources"])
+def test_layer_state_hot_update_reaches_device_routing(cuda, per_token):
+    """The op reads M from the reference's layer state (a stand-in with its
+    fields) on every call: a hot update written by the reference's controller
+    (expert_swap.py:10963-10972), with no call into this package, changes the
+    next forward's routing, bit-exact against the oracle."""
+    from tests.layer_state_standin import StandInLayerState
+
+    placemoe_amd.apply_veomni_fused_moe_patch("hip")
+    wl = make_workload("fold", tokens=192)
+    L = wl.slot_to_logical
+    M0 = wl.mapping.numpy()
+    M1 = _rotated_mapping(L, M0)
+    rank = 3
+    state = StandInLayerState(key="layers.5.mlp.experts", num_experts=wl.num_experts,
+                              logical_to_physical=torch.as_tensor(wl.owner_slots()),
+                              slot_to_logical=torch.as_tensor(L), source_logical_to_physical=torch.as_tensor(M0))
+    placement = LayerPlacement.from_layer_state(state, source_rank=rank)
+    if per_token:
+        placement.token_sources = wl.sources.to(cuda)
+    src = wl.sources.numpy() if per_token else np.full(wl.T, rank)
+    fc1, fc2 = wl.fc1.to(cuda), wl.fc2.to(cuda)
+    PLACEMENTS.register(placement, fc1, fc2)
+    try:
+        for step, M in enumerate((M0, M1)):
+            if step == 1:
+                assert state.hot_update(M1) == 1
+                assert placement.placement_version == 1
+            placement.clear_slot_tokens()
+            phys = O.map_logical_to_physical(M, src, wl.selected.numpy())
+            dev_M = placement.mapping_for_device(cuda)
+            r = kernels.route(wl.selected.to(cuda), wl.C, mapping=dev_M, sources=placement.token_sources,
+                              source=placement.source)
+            assert_exact(r.phys, phys, f"phys step {step}")
+            assert_exact(r.pos, O.scatter_index(phys), f"pos step {step}")
+            out = placemoe_amd.fused_moe_forward(
+                num_experts=wl.num_experts, routing_weights=wl.routing_weights.to(cuda),
+                selected_experts=wl.selected.to(cuda), hidden_states=wl.hidden.to(cuda), fc1_1_weight=None,
+                fc1_2_weight=None, fc2_weight=fc2, fc1_1_2_weight=fc1)
+            fwd = O.moe_layer_forward(wl.hidden, wl.routing_weights, phys, wl.fc1, wl.fc2)
+            assert_exact(placement.accumulated_slot_tokens, fwd["counts"], f"slot tokens step {step}")
+            assert_bf16_close(out, fwd["out"], name=f"output step {step}")
+    finally:
+        PLACEMENTS.clear()
+
+
 def test_materialize_copy_weights_on_device(cuda):
     # parallel_plan.py:114-123: W_copy[c] = W_logical[L[c]], zeros where L[c] == -1.
     g = torch.Generator(device=cuda).manual_seed(3)
@@ -103,6 +149,9 @@ def test_out_of_range_expert_id_raises(cuda, monkeypatch):
     sel[5, 1] = wl.C  # one past the last expert
     sel = sel.to(cuda)
     out = _bad_call(cuda, wl, sel)
+    # The backward looks at the status copy without waiting for it; once it
+    # has landed (here: after a synchronisation) the backward raises.
+    torch.cuda.synchronize()
     with pytest.raises(ValueError, match="outside"):
         out.sum().backward()
     # a valid call afterwards is unaffected
@@ -127,6 +176,24 @@ def test_forward_only_bad_id_is_reported_by_a_later_call(cuda, monkeypatch):
             _bad_call(cuda, wl, wl.selected.to(cuda))
         _bad_call(cuda, wl, wl.selected.to(cuda))  # reported once
     experts._PENDING_CHECKS.clear()
+
+
+def test_pending_bad_id_is_reported_by_check_pending_routes(cuda, monkeypatch):
+    """check_pending_routes(block=True) waits for the status copies and raises;
+    without block it raises only for copies that have landed."""
+    placemoe_amd.apply_veomni_fused_moe_patch("hip")
+    monkeypatch.delenv("PLACEMOE_AMD_CHECK_ROUTES", raising=False)
+    wl = make_workload("toy", tokens=64)
+    sel = wl.selected.clone()
+    sel[3, 0] = -1
+    with torch.no_grad():
+        _bad_call(cuda, wl, sel.to(cuda))
+        with pytest.raises(ValueError, match="outside"):
+            experts.check_pending_routes(block=True)
+        experts.check_pending_routes(block=True)  # reported once
+        _bad_call(cuda, wl, wl.selected.to(cuda))
+        experts.check_pending_routes(block=True)
+    assert not experts._PENDING_CHECKS
 
 
 def test_fold_skips_and_flags_out_of_range_copy_slots(cuda):
