@@ -57,8 +57,11 @@ HIP_FLAGS = [
 RESOURCE_CHECKED = {"grouped_gemm.hip": re.compile(r"grouped_gemm")}
 RESOURCE_FLAG = "-Rpass-analysis=kernel-resource-usage"
 
-# name -> (source, extra flags): library variants for tests.
-VARIANTS = {"tiletab2": ("grouped_gemm.hip", ["-DPMX_TILE_TAB=2"])}
+# name -> (source, extra flags): library variants for tests and comparisons.
+#   tiletab2: a two-entry LDS tile table (the on-the-spot tile decode runs at small shapes);
+#   w8:       the eight-wave GEMM kernel for every call (the four-wave kernel switched off).
+VARIANTS = {"tiletab2": ("grouped_gemm.hip", ["-DPMX_TILE_TAB=2"]),
+            "w8": ("grouped_gemm.hip", ["-DPMX_GEMM_W4=0"])}
 VARIANT_DIR = LIB_DIR / "variants"
 
 

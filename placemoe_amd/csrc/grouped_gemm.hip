@@ -830,10 +830,10 @@ __device__ __forceinline__ void setup_operands(const GemmParams& P, Tile<KIND, B
 }
 
 // Zero gradient tile of an empty group (wgrad): 16-byte stores, no LDS.
-template <int BM>
+template <int BM, int NT = NTHREADS>
 __device__ __forceinline__ void zero_tile(const GemmParams& P, const TileInfo& ti, int t) {
   const uint4 z = make_uint4(0, 0, 0, 0);
-  for (int e = t; e < BM * (BN / 8); e += NTHREADS) {
+  for (int e = t; e < BM * (BN / 8); e += NT) {
     const int64_t m = (int64_t)ti.mtile * BM + e / (BN / 8);
     const int64_t n = (int64_t)ti.ntile * BN + (e % (BN / 8)) * 8;
     if (m < P.M && n < P.N) {
@@ -956,7 +956,7 @@ __device__ __forceinline__ void block_barrier() {
 // rows; measured slower on every shape.  Alternating the direction of the
 // deal from round to round keeps the rounds but balances less: on the
 // DeepSeek-V3-shape share 96% against 98% of the mean per block.)  Needs a
-// grid of whole XCDs and G <= NTHREADS; otherwise (false) the plain order
+// grid of whole XCDs and G <= NT (the block's threads); otherwise (false) the plain order
 // is used.  Rounds past what the LDS holds alternate direction.
 constexpr int kBandTiles = 32;
 constexpr int kNumXcd = 8;
@@ -965,6 +965,7 @@ constexpr int kNumXcd = 8;
 // `deal[r]` (bytes after nk[G]) = the band of round r, 0..7 within the round,
 // that XCD `xcd` takes, for the first `cap` rounds (the return value).
 // `costs` is scratch of `cost_slots` int32 (LDS not yet in use).
+template <int NT = NTHREADS>
 __device__ __noinline__ int32_t build_wgrad_order(const GemmParams& P, int32_t* nk, int32_t* order, int t,
                                                   int64_t total, int64_t tiles_per_group, int32_t xcd,
                                                   int32_t* costs, int32_t cost_slots) {
@@ -988,7 +989,7 @@ __device__ __noinline__ int32_t build_wgrad_order(const GemmParams& P, int32_t* 
   int64_t cap = (int64_t)(kMaxGroups + 1 - G) * 4;
   if (cap > cost_slots / kNumXcd) cap = cost_slots / kNumXcd;
   if (cap > rounds) cap = rounds;
-  for (int64_t b = t; b < cap * kNumXcd; b += NTHREADS) {
+  for (int64_t b = t; b < cap * kNumXcd; b += NT) {
     const int64_t tile = b * kBandTiles;
     costs[b] = tile < total ? nk[order[tile / tiles_per_group]] : 0;
   }
@@ -1012,6 +1013,40 @@ __device__ __noinline__ int32_t build_wgrad_order(const GemmParams& P, int32_t* 
   }
   __syncthreads();
   return (int32_t)cap;
+}
+
+// Exclusive prefix of m-tiles (BM rows) per group into tpre[0..G]: GPT groups
+// per thread, then a block scan of the NT partial sums in scan_buf.
+template <int BM, int NT>
+__device__ __forceinline__ void group_prefix(const GemmParams& P, int32_t* tpre, int32_t* scan_buf, int t) {
+  constexpr int GPT = kMaxGroups / NT;
+  const int G = P.G;
+  int32_t loc[GPT];
+  int32_t sum = 0;
+#pragma unroll
+  for (int i = 0; i < GPT; ++i) {
+    const int g = t * GPT + i;
+    int32_t v = 0;
+    if (g < G) v = (P.offsets[g + 1] - P.offsets[g] + BM - 1) / BM;
+    loc[i] = sum;
+    sum += v;
+  }
+  scan_buf[t] = sum;
+  __syncthreads();
+  for (int off = 1; off < NT; off <<= 1) {
+    const int32_t add = t >= off ? scan_buf[t - off] : 0;
+    __syncthreads();
+    scan_buf[t] += add;
+    __syncthreads();
+  }
+  const int32_t base = scan_buf[t] - sum;
+#pragma unroll
+  for (int i = 0; i < GPT; ++i) {
+    const int g = t * GPT + i;
+    if (g < G) tpre[g] = base + loc[i];
+  }
+  if (t == NT - 1) tpre[G] = scan_buf[NT - 1];
+  __syncthreads();
 }
 
 // One block per CU walks its tiles (slot, slot + grid, ...) as one stream of
@@ -1082,35 +1117,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
     }
   } else {
     ntn = (KIND == KIND_FC1) ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
-    // Exclusive prefix of m-tiles per group: GPT groups per thread, then a
-    // block scan of the NTHREADS partial sums.
-    constexpr int GPT = kMaxGroups / NTHREADS;
-    int32_t loc[GPT];
-    int32_t sum = 0;
-#pragma unroll
-    for (int i = 0; i < GPT; ++i) {
-      const int g = t * GPT + i;
-      int32_t v = 0;
-      if (g < G) v = (P.offsets[g + 1] - P.offsets[g] + BM - 1) / BM;
-      loc[i] = sum;
-      sum += v;
-    }
-    scan_buf[t] = sum;
-    __syncthreads();
-    for (int off = 1; off < NTHREADS; off <<= 1) {
-      const int32_t add = t >= off ? scan_buf[t - off] : 0;
-      __syncthreads();
-      scan_buf[t] += add;
-      __syncthreads();
-    }
-    const int32_t base = scan_buf[t] - sum;
-#pragma unroll
-    for (int i = 0; i < GPT; ++i) {
-      const int g = t * GPT + i;
-      if (g < G) tpre[g] = base + loc[i];
-    }
-    if (t == NTHREADS - 1) tpre[G] = scan_buf[NTHREADS - 1];
-    __syncthreads();
+    group_prefix<BM, NTHREADS>(P, tpre, scan_buf, t);
     total = (int64_t)tpre[G] * ntn;
   }
 
@@ -1380,6 +1387,724 @@ __global__ __launch_bounds__(NTHREADS, 1) void grouped_gemm_kernel(GemmParams P)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Four-wave kernel (FAST loads only).
+//
+// The same persistent walk as grouped_gemm_kernel - band order, LDS tile
+// table, balanced weight-gradient deal, one stream of 64-deep K-tiles through
+// two 64 KB stages filled by buffer->LDS loads - with 4 waves, one per SIMD,
+// in a 2 x 2 arrangement, each owning 128 x 128 of the 256 x 256 output tile
+// as 8 x 8 tiles of v_mfma_f32_16x16x32_bf16 (256 accumulator registers per
+// lane, in AGPRs).  Per K-tile the waves read 128 KB of fragments from LDS
+// (the 8-wave layout: 192 KB), and a 16 x 16 accumulator moves half the
+// register bytes per flop of a 32 x 32 one, which at the part's power limit
+// lets the matrix cores run at a higher clock.  A K-tile is two 32-deep
+// k-steps of 64 MFMAs; the MFMAs run one k-step behind the fragment reads, so
+// each K-tile's single block barrier falls between two k-steps of MFMAs and
+// every wave multiplies from registers right after it.  The next K-tile's 16
+// loads per wave go one per MFMA group, half in each k-step.
+// ---------------------------------------------------------------------------
+namespace w4 {
+
+// Kinds (bit KIND) whose next K-tile's loads all go among the first k-step's
+// MFMAs (a whole K-tile less half a k-step to land) instead of half in each
+// k-step.  Measured in the layer (config 3 / the Qwen3 shape, ms): fc1 +
+// SwiGLU 3.10 -> 3.02-3.05 / 0.85 -> 0.81, fc2 dgrad 1.80 -> 1.74-1.76 /
+// 0.53 -> 0.49-0.50, fc1 wgrad 3.31-3.34 -> 2.89-2.90 / 0.82 -> 0.78-0.79.
+// Two loads per MFMA group in the first half of the k-step instead: 2-10%
+// slower.  (The fc2 forward spills four VGPRs that way; it runs on the
+// eight-wave kernel.)
+#ifndef PMX_W4_LOADS_FIRST_HALF
+#define PMX_W4_LOADS_FIRST_HALF 29
+#endif
+
+constexpr int NW = 4, NT = 64 * NW;
+constexpr int BM = 256;
+constexpr int FM = 8, FN = 8;                // 16 x 16 accumulator tiles per wave
+constexpr int QO = BM * BK * 2 / 1024 / NW;  // loads per wave, operand and K-tile (8)
+constexpr int STAGE_BYTES = (BM + BN) * BK * 2;
+constexpr int B_OFF = BM * BK * 2;  // B's region within a stage
+static_assert(BM == BN, "square block tiles");
+
+// M/N-contiguous tiles ([64 k][256]): 16-byte chunk c of k-row kk is stored at
+// c ^ mn_swz(kk), so that the 4 k-rows and the two 8-row k-blocks that one
+// half-wave's transposing fragment read touches fall on distinct banks.
+__device__ __forceinline__ int mn_swz(int kk) { return (4 * (kk & 3)) ^ (2 * ((kk >> 3) & 1)); }
+
+// Operand of one output tile: descriptors and this wave's per-lane load
+// offsets.  Load q0 (0 .. QO-1) of a K-tile covers 1 KB of the stage at chunk
+// q0 * NW + wave of the operand's region; its per-lane offset is off[q0 & 1]
+// and the rest, (q0 >> SHIFT) * step plus the K-tile advance, goes into the
+// instruction's scalar offset (SHIFT is 1 for fc1's weights, else 0): no
+// per-load vector arithmetic, two offsets per operand.  The range check covers
+// the sum of both offsets.  A lane whose chunk lies outside the operand's
+// columns holds kOOB; for the weight gradient kOOB plus a large scalar offset
+// may wrap into the descriptor, which loads other columns of the operand
+// into that lane's slot - they feed only output columns that are never
+// written.
+struct Op {
+  __amdgpu_buffer_rsrc_t r0, r1;  // r1: fc1's up rows (loads with odd q0)
+  uint32_t ldb;                   // bytes between consecutive (k-)rows
+  uint32_t step;                  // offset per step of q0 >> SHIFT
+  uint32_t off[2];                // per-lane offset of loads with even / odd q0
+};
+
+template <int KIND>
+struct Tile {
+  TileInfo i;
+  Op A, B;
+};
+
+// K-contiguous operand: load q fills rows 8q .. 8q+7, lane i row 8q + i/8,
+// physical chunk i%8 = logical chunk ^ kc_swz(row).  With q = q0 * NW + wave
+// the row's swizzle does not depend on q0 (kc_swz(row) = (i/16 + 4 wave) % 8),
+// so load q0's offset is load 0's plus q0 * 32 rows.
+__device__ __forceinline__ void kc_offs(Op& op, int wave, int lane) {
+  const int row = wave * 8 + (lane >> 3);
+  const int c = (lane & 7) ^ kc_swz(row);
+  op.off[0] = op.off[1] = (uint32_t)row * op.ldb + (uint32_t)c * 16u;
+  op.step = 32u * op.ldb;
+}
+
+// M/N-contiguous operand, columns col0 .. col0+255: load q fills k-rows 2q,
+// 2q+1; lane i k-row 2q + i/32, physical chunk i%32 = logical chunk ^
+// mn_swz(k-row).  With q = q0 * NW + wave the swizzle depends on q0 only
+// through its parity (bit 3 of the k-row), so there are two column offsets.
+// KT_ROW: the offset counts the k-row within the K-tile (q0 adds 8 rows);
+// else within the load (the K-tile advance includes the load's rows).
+template <bool KT_ROW>
+__device__ __forceinline__ void mn_offs(Op& op, int wave, int lane, int64_t col0, int64_t ncols) {
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    const int krow = (par * NW + wave) * 2 + (lane >> 5);
+    const int c = (lane & 31) ^ mn_swz(krow);
+    const int64_t col = col0 + c * 8;
+    const uint32_t r = KT_ROW ? (uint32_t)((wave * 2) + (lane >> 5)) : (uint32_t)(lane >> 5);
+    // load q0 = par: its k-row (KT_ROW) is r + 8 * par, counted by the step
+    op.off[par] = col < ncols ? r * op.ldb + (uint32_t)col * 2u : kOOB;
+  }
+  op.step = KT_ROW ? 8u * op.ldb : 0u;
+}
+
+// Describe the operands of one output tile (FAST: K a multiple of 64 and the
+// dgrad weights one tensor; weight gradient: its operands within 31-bit
+// offsets, one descriptor per group).
+template <int KIND>
+__device__ __forceinline__ void setup(const GemmParams& P, Tile<KIND>& tc, int wave, int lane) {
+  asm volatile("" : "+v"(lane));  // keep the per-lane arithmetic here (see epilogue)
+  const TileInfo& ti = tc.i;
+  if constexpr (KIND == KIND_TN) {
+    const int64_t rows = ti.row_end - ti.row0;
+    tc.A.ldb = (uint32_t)(P.a.ld * 2);
+    tc.B.ldb = (uint32_t)(P.b.ld * 2);
+    tc.A.r0 = tc.A.r1 = make_rsrc(P.a.p0 + (int64_t)ti.row0 * P.a.ld, (uint64_t)rows * P.a.ld * 2);
+    tc.B.r0 = tc.B.r1 = make_rsrc(P.b.p0 + (int64_t)ti.row0 * P.b.ld, (uint64_t)rows * P.b.ld * 2);
+    mn_offs<true>(tc.A, wave, lane, (int64_t)ti.mtile * BM, P.M);
+    mn_offs<true>(tc.B, wave, lane, (int64_t)ti.ntile * BN, P.N);
+  } else {
+    const int64_t rows = ti.row_end - ti.row0 < BM ? ti.row_end - ti.row0 : BM;
+    tc.A.ldb = (uint32_t)(P.a.ld * 2);
+    tc.A.r0 = tc.A.r1 = make_rsrc(P.a.p0 + (int64_t)ti.row0 * P.a.ld, (uint64_t)rows * P.a.ld * 2);
+    kc_offs(tc.A, wave, lane);
+    const bf16_t* b0 = P.b.p0 + (int64_t)ti.g * P.b.gs0;
+    if constexpr (KIND == KIND_FC1) {
+      // Virtual B rows: per 64 rows, 32 gate rows then the matching 32 up rows.
+      // Load q covers rows 8q .. 8q+7: block q/8 = q0/2, up rows exactly when
+      // q % 8 >= 4, i.e. when q0 is odd; row & 31 = 8 wave + i/8 for every q0.
+      // So load q0 reads intermediate row j0 + 32 (q0/2) of the gate (even
+      // q0) or up (odd q0) weights, j0 = 128 ntile + 8 wave + i/8; rows past
+      // I fail the descriptor's range check.
+      tc.B.r0 = make_rsrc(b0, (uint64_t)P.I * P.K * 2);
+      tc.B.r1 = make_rsrc(P.b.p1 + (int64_t)ti.g * P.b.gs1, (uint64_t)P.I * P.K * 2);
+      tc.B.ldb = (uint32_t)(P.K * 2);
+      const int64_t j0 = (int64_t)ti.ntile * 128 + wave * 8 + (lane >> 3);
+      const int row = wave * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ kc_swz(row);
+      tc.B.step = 32u * tc.B.ldb;
+      tc.B.off[0] = tc.B.off[1] = j0 < P.I ? (uint32_t)j0 * tc.B.ldb + (uint32_t)c * 16u : kOOB;
+    } else if constexpr (KIND == KIND_NT) {
+      const int64_t n0 = (int64_t)ti.ntile * BN;
+      tc.B.r0 = tc.B.r1 = make_rsrc(b0 + n0 * P.K, (uint64_t)(P.N - n0) * P.K * 2);
+      tc.B.ldb = (uint32_t)(P.K * 2);
+      kc_offs(tc.B, wave, lane);
+    } else {
+      // NN / NNS: B[g] is [K][N] in one tensor.
+      tc.B.r0 = tc.B.r1 = make_rsrc(b0, (uint64_t)P.K * P.N * 2);
+      tc.B.ldb = (uint32_t)(P.N * 2);
+      mn_offs<false>(tc.B, wave, lane, (int64_t)ti.ntile * BN, P.N);
+    }
+  }
+}
+
+// Load J of this wave's share of K-tile kt (A: 0 .. QO-1, B: QO .. 2QO-1).
+// Every offset stays within its descriptor or fails the range check; kt is
+// always a K-tile of the tile (a finished cursor re-loads K-tile 0).
+template <int KIND, int J>
+__device__ __forceinline__ void issue(char* stage, const Tile<KIND>& tc, int32_t kt, int wave) {
+  constexpr int q0 = J % QO;
+  const int q = q0 * NW + wave;
+  if constexpr (J < QO) {
+    const uint32_t soff = KIND == KIND_TN ? (uint32_t)kt * BK * tc.A.ldb : (uint32_t)kt * (BK * 2);
+    dma16(tc.A.r0, stage + q * 1024, tc.A.off[q0 & 1], soff + (uint32_t)q0 * tc.A.step);
+  } else {
+    char* dst = stage + B_OFF + q * 1024;
+    if constexpr (KIND == KIND_TN) {
+      dma16(tc.B.r0, dst, tc.B.off[q0 & 1], (uint32_t)kt * BK * tc.B.ldb + (uint32_t)q0 * tc.B.step);
+    } else if constexpr (KIND == KIND_NN || KIND == KIND_NNS) {
+      dma16(tc.B.r0, dst, tc.B.off[q0 & 1], ((uint32_t)kt * BK + (uint32_t)(q * 2)) * tc.B.ldb);
+    } else if constexpr (KIND == KIND_FC1) {
+      dma16((q0 & 1) ? tc.B.r1 : tc.B.r0, dst, tc.B.off[q0 & 1], (uint32_t)kt * (BK * 2) + (uint32_t)(q0 >> 1) * tc.B.step);
+    } else {
+      dma16(tc.B.r0, dst, tc.B.off[q0 & 1], (uint32_t)kt * (BK * 2) + (uint32_t)q0 * tc.B.step);
+    }
+  }
+}
+
+struct Frags {
+  bf16x8_t a[FM], b[FN];
+};
+
+// The lane index recomputed where it is needed (two instructions) instead of
+// kept in a register through the whole kernel.
+__device__ __forceinline__ int lane_id() { return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+// Per-lane byte offsets of the wave's fragments within an operand's region of
+// a stage, computed once per tile so that a fragment read is one address
+// addition plus an immediate offset.
+//   K-contiguous operand: lane l reads row rb + l%16 (rb = 16 * fragment +
+//   128 * wave row), chunk ks*4 + l/16; kc_swz(rb + l%16) = kc_swz(l%16), so
+//   the offset is rb*128 + o[ks].
+//   M/N-contiguous operand (256-wide, mn_swz): fragment n is columns
+//   w*128 + 16n .. +15 (w: the wave's column); lane l (group g = l/16, i =
+//   l%16) addresses k-row ks*32 + 8g + 4h + i/4 (h: which of the two
+//   transposing reads) and columns 4(i%4) .. +3; mn_swz of that k-row is
+//   4 ((i/4) % 4) ^ 2 (g % 2) whatever ks and h, so the offset is
+//   o[n] + ks*16384 + h*2048.
+template <bool MN>
+struct Slots {
+  int32_t o[MN ? FN : 2];
+};
+
+template <bool MN>
+__device__ __forceinline__ void make_slots(Slots<MN>& sl, int w, int lane) {
+  if constexpr (!MN) {
+    const int r = lane & 15;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) sl.o[ks] = r * (BK * 2) + (((ks * 4 + (lane >> 4)) ^ kc_swz(r)) << 4);
+  } else {
+    const int g = lane >> 4, i = lane & 15;
+    const int s = mn_swz(g * 8 + (i >> 2));
+    const int base = (g * 8 + (i >> 2)) * (2 * BN) + (i & 1) * 8;
+#pragma unroll
+    for (int n = 0; n < FN; ++n) {
+      const int c = w * 16 + n * 2 + ((i & 3) >> 1);
+      sl.o[n] = base + ((c ^ s) << 4);
+    }
+  }
+}
+
+// Fragment (J-th of its operand) at a slot: K-contiguous rows rb .. rb+15;
+// M/N-contiguous from two transposing reads (within each 16-lane group lane
+// i receives column i of the 4 x 16 block the group addresses).
+__device__ __forceinline__ bf16x8_t frag_kc(const char* t, int rb, int32_t o) {
+  return *reinterpret_cast<const bf16x8_t*>(t + rb * (BK * 2) + o);
+}
+__device__ __forceinline__ bf16x8_t frag_mn(const char* t, int ks, int32_t o) {
+  const char* p = t + ks * 32 * (2 * BN) + o;
+  const bf16x4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_TR_PTR(p));
+  const bf16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_TR_PTR(p + 4 * (2 * BN)));
+  return bf16x8_t{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+}
+
+template <int KIND>
+struct TileSlots {
+  Slots<a_is_mn<KIND>()> a;
+  Slots<b_is_mn<KIND>()> b;
+};
+
+template <int KIND>
+__device__ __forceinline__ TileSlots<KIND> tile_slots(int wm, int wn, int lane) {
+  TileSlots<KIND> ts;
+  make_slots(ts.a, wm, lane);
+  make_slots(ts.b, wn, lane);
+  return ts;
+}
+
+// Fragment J of k-step ks: A fragments 0 .. FM-1, then B fragments.
+template <int KIND, int J>
+__device__ __forceinline__ void read_frag(const char* stage, int ks, int wm, int wn, const TileSlots<KIND>& ts,
+                                          Frags& f) {
+  if constexpr (J < FM) {
+    if constexpr (a_is_mn<KIND>()) f.a[J] = frag_mn(stage, ks, ts.a.o[J]);
+    else f.a[J] = frag_kc(stage, wm * 128 + J * 16, ts.a.o[ks]);
+  } else {
+    if constexpr (b_is_mn<KIND>()) f.b[J - FM] = frag_mn(stage + B_OFF, ks, ts.b.o[J - FM]);
+    else f.b[J - FM] = frag_kc(stage + B_OFF, wn * 128 + (J - FM) * 16, ts.b.o[ks]);
+  }
+}
+
+// The I-th read of a k-step, in the order the (mt-major) MFMAs consume the
+// fragments: A0, B0 .. B7, A1 .. A7.
+constexpr int frag_order(int i) { return i == 0 ? 0 : i <= FN ? FM + i - 1 : i - FN; }
+
+// MFMAs I .. I+N-1 of a k-step (index mt * FN + nt).  FIRST: from zero.  The
+// B fragment goes first, so each accumulator holds its 16 x 16 output tile
+// transposed: lane l holds output row l%16, columns 4*(l/16) .. +3.
+template <int I, int N, bool FIRST = false>
+__device__ __forceinline__ void mfma(const Frags& f, f32x4_t (&acc)[FM][FN]) {
+#pragma unroll
+  for (int x = I; x < I + N; ++x)
+    acc[x / FN][x % FN] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.b[x % FN], f.a[x / FN],
+                                                                   FIRST ? f32x4_t{} : acc[x / FN][x % FN], 0, 0, 0);
+}
+
+// Epilogue staging: a round is 64 of the wave's 128 rows; row r (0 .. 63) is
+// 256 bytes (the wave's 128 columns) in 1 KB chunk (r/4) * NW + wave of the
+// freed stage - the chunks this wave's own loads fill, so no other wave
+// touches them - at offset (r%4) * 256, with 16-byte piece c at c ^ (r%16)
+// (conflict-free 8-byte writes and 16-byte reads).
+__device__ __forceinline__ int stg_off(int wave, int r, int c) {
+  return ((r >> 2) * NW + wave) * 1024 + (r & 3) * 256 + ((c ^ (r & 15)) << 4);
+}
+
+// Stage tiles mt = 4*round .. +3, tiles nt = 0 .. NC-1 of the wave:
+// v(mt, nt) returns the lane's four values (row l%16, columns 4*(l/16) .. +3
+// of the tile) as four bf16; tile nt goes to the 16-column block blk(nt).
+template <int NC, typename F, typename B>
+__device__ __forceinline__ void stage_round(char* stage, int wave, int lane, int round, F v, B blk) {
+  const int r16 = lane & 15, h = lane >> 4;
+#pragma unroll
+  for (int mtl = 0; mtl < 4; ++mtl) {
+#pragma unroll
+    for (int nt = 0; nt < NC; ++nt) {
+      const int r = mtl * 16 + r16;
+      const int x = blk(nt) * 32 + h * 8;  // byte of the 256-byte row
+      *reinterpret_cast<uint2*>(stage + stg_off(wave, r, x >> 4) + (x & 15)) = v(4 * round + mtl, nt);
+    }
+    // one row of tiles at a time: the scheduler would otherwise read all of
+    // the round's accumulators into VGPRs before the first write
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+__device__ __forceinline__ uint4 staged(const char* stage, int wave, int r, int c) {
+  return *reinterpret_cast<const uint4*>(stage + stg_off(wave, r, c));
+}
+
+__device__ __forceinline__ uint2 bf16x4(const f32x4_t& a) { return make_uint2(pack2(a[0], a[1]), pack2(a[2], a[3])); }
+
+// Write out the wave's 128 x 128 share of a finished tile (two rounds of 64
+// rows), with the kind's epilogue arithmetic - the same rounding points as
+// grouped_gemm_kernel's epilogue.  Store q of a round covers 4 rows x 256
+// bytes: lane l row q*4 + l/16, 16-byte piece l%16.
+template <int KIND>
+__device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti, int wm, int wn, int wave, int lane,
+                                         const f32x4_t (&acc)[FM][FN], char* stage) {
+  asm volatile("" : "+v"(lane));
+  const int cc = lane & 15, rq = lane >> 4;
+  // Top-1 row map (KIND_NT, KIND_NN): the wave's 128 row targets (and the
+  // rows' router weights) are loaded before the first store, since one
+  // counter tracks this wave's loads and stores in issue order: lane l holds
+  // those of rows l and 64 + l, and a store's lanes fetch theirs with a
+  // cross-lane read.  Targets outside [0, M) are not written.
+  const bool mapped = (KIND == KIND_NT || KIND == KIND_NN) && P.row_tok != nullptr;
+  int32_t tok2[2] = {-1, -1};
+  uint32_t wt2[2] = {0, 0};
+  if constexpr (KIND == KIND_NT || KIND == KIND_NN) {
+    if (mapped) {
+      const int64_t r0 = ti.row0 + wm * 128;
+      const int32_t nrows = (int32_t)(ti.row_end - r0 < 0 ? 0 : (ti.row_end - r0 > 128 ? 128 : ti.row_end - r0));
+      const __amdgpu_buffer_rsrc_t rt = make_rsrc(P.row_tok + r0, (uint64_t)nrows * 4);
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(P.row_w + r0, (uint64_t)nrows * 2);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = h * 64 + lane;
+        const int32_t tok = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rt, (uint32_t)r * 4u, 0, 0);
+        tok2[h] = r < nrows ? tok : -1;
+        if constexpr (KIND == KIND_NT) wt2[h] = __builtin_amdgcn_raw_buffer_load_b16(rw, (uint32_t)r * 2u, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+    // Rounds stay apart in the schedule: hoisting the next round's
+    // accumulator reads and conversions would hold their registers.
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t rb = wm * 128 + round * 64;  // first tile row of the round
+    if constexpr (KIND == KIND_FC1) {
+      // The wave's 128 virtual columns: gate tiles nt = 0,1,4,5 and their up
+      // tiles nt + 2, for intermediate columns jb .. jb+63.  Staged as
+      // [gate 64 | up 64] (gu), then act = bf16(bf16(silu(gate)) * up).
+      const int64_t I = P.I;
+      const int64_t jb = (int64_t)ti.ntile * 128 + wn * 64;
+      stage_round<FN>(stage, wave, lane, round, [&](int mt, int nt) { return bf16x4(acc[mt][nt]); },
+                      [](int nt) { return ((nt & 2) ? 4 : 0) + (nt >> 2) * 2 + (nt & 1); });
+      {
+        const OutWin w = out_window(P.gu, ti.row0 + rb, ti.row_end, 2 * I);
+        const int64_t j = jb + (cc & 7) * 8;
+        const uint32_t voff = j < I ? (uint32_t)rq * w.rowb + (uint32_t)((cc < 8 ? 0 : I) + j) * 2u : kOOB;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          win_store(w, voff, q * 4, staged(stage, wave, q * 4 + rq, cc));
+          if (q % 8 == 7) __builtin_amdgcn_sched_barrier(0);  // at most 8 staged reads in flight
+        }
+      }
+      stage_round<4>(stage, wave, lane, round, [&](int mt, int k) {
+        const int ng = (k >> 1) * 4 + (k & 1);
+        float g[4], u[4];
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          g[e] = acc[mt][ng][e], g[e + 1] = acc[mt][ng][e + 1];
+          u[e] = acc[mt][ng + 2][e], u[e + 1] = acc[mt][ng + 2][e + 1];
+          round2_bf16(g[e], g[e + 1]);
+          round2_bf16(u[e], u[e + 1]);
+          g[e] = silu_f32(g[e]), g[e + 1] = silu_f32(g[e + 1]);
+          round2_bf16(g[e], g[e + 1]);
+        }
+        return pack4(g[0] * u[0], g[1] * u[1], g[2] * u[2], g[3] * u[3]);
+      }, [](int k) { return k; });
+      {
+        // act: 64 rows x 128 bytes; store q covers 8 rows, lane l row q*8 + l/8, piece l%8.
+        const OutWin w = out_window(P.act, ti.row0 + rb, ti.row_end, I);
+        const int c8 = lane & 7;
+        const int64_t j = jb + c8 * 8;
+        const uint32_t voff = j < I ? (uint32_t)(lane >> 3) * w.rowb + (uint32_t)j * 2u : kOOB;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) win_store(w, voff, q * 8, staged(stage, wave, q * 8 + (lane >> 3), c8));
+      }
+    } else if constexpr (KIND == KIND_NNS) {
+      // fc2 dgrad: the tile is dact (bf16, as the reference stores it) for
+      // columns j < I; with the forward's gate/up of the same rows it becomes
+      // [d_gate | d_up] of dG1.  Each half round's gate/up loads go out before
+      // its staging reads.
+      const int64_t I = P.I;
+      const int64_t j = (int64_t)ti.ntile * BN + wn * 128 + cc * 8;
+      const OutWin wi = out_window(P.gin, ti.row0 + rb, ti.row_end, 2 * I);
+      const OutWin wo = out_window(P.c0, ti.row0 + rb, ti.row_end, 2 * I);
+      const uint32_t vg = j < I ? (uint32_t)rq * wi.rowb + (uint32_t)j * 2u : kOOB;
+      const uint32_t vu = vg + (uint32_t)I * 2u;
+      stage_round<FN>(stage, wave, lane, round, [&](int mt, int nt) { return bf16x4(acc[mt][nt]); },
+                      [](int nt) { return nt; });
+#pragma unroll
+      for (int hr = 0; hr < 2; ++hr) {
+        uint4 gv[8], uv[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          gv[q] = win_load(wi, vg, (hr * 8 + q) * 4);
+          uv[q] = win_load(wi, vu, (hr * 8 + q) * 4);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int r = (hr * 8 + q) * 4;
+          const uint4 v = staged(stage, wave, r + rq, cc);
+          float d[8], g[8], u[8], dg[8], du[8];
+          unpack8(v, d);
+          unpack8(gv[q], g);
+          unpack8(uv[q], u);
+          swiglu_bwd8(d, g, u, dg, du);
+          win_store(wo, vg, r, pack8(dg));
+          win_store(wo, vu, r, pack8(du));
+        }
+        asm volatile("" ::: "memory");
+      }
+    } else if constexpr (KIND == KIND_TN) {
+      // Rows m of copy g's gradient: those below csplit in c0, the rest in
+      // c1 (split fc1), each tensor through a descriptor over the copy's rows
+      // in it (the host sends a copy of more than 2 GiB to the 8-wave kernel).
+      stage_round<FN>(stage, wave, lane, round, [&](int mt, int nt) { return bf16x4(acc[mt][nt]); },
+                      [](int nt) { return nt; });
+      const int64_t col = (int64_t)ti.ntile * BN + wn * 128 + cc * 8;
+      const int64_t m0 = (int64_t)ti.mtile * BM + rb;  // first gradient row of the round
+      const int64_t rows0 = P.csplit < P.M ? P.csplit : P.M;
+      const OutWin w0 = {make_rsrc(P.c0 + ti.g * P.cgs, (uint64_t)rows0 * P.ldc * 2), (uint32_t)(P.ldc * 2)};
+      const OutWin w1 = {make_rsrc(P.c1 + ti.g * P.cgs, (uint64_t)(P.M - rows0) * P.ldc * 2), (uint32_t)(P.ldc * 2)};
+      const int64_t m = m0 + rq;  // the lane's row of store 0
+      const bool cin = col < P.N;
+      const bool split = uni(m0 + 63 >= rows0 ? 1 : 0) != 0;  // some row of the round lies in c1
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const uint4 v = staged(stage, wave, q * 4 + rq, cc);
+        const int64_t mq = m + q * 4;
+        const uint32_t o0 = cin && mq < rows0 ? (uint32_t)mq * w0.rowb + (uint32_t)col * 2u : kOOB;
+        win_store(w0, o0, 0, v);
+        if (split) {
+          const uint32_t o1 = cin && mq >= rows0 ? (uint32_t)(mq - rows0) * w1.rowb + (uint32_t)col * 2u : kOOB;
+          win_store(w1, o1, 0, v);
+        }
+        if (q % 8 == 7) __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      const int64_t col = (int64_t)ti.ntile * BN + wn * 128 + cc * 8;
+      stage_round<FN>(stage, wave, lane, round, [&](int mt, int nt) { return bf16x4(acc[mt][nt]); },
+                      [](int nt) { return nt; });
+      const OutWin w = out_window(P.c0, ti.row0 + rb, ti.row_end, P.ldc);
+      const uint32_t voff = col < P.N ? (uint32_t)rq * w.rowb + (uint32_t)col * 2u : kOOB;
+      // Mapped rows go to row dst of the whole output (dst is -1 for rows
+      // past the tile's group): through one descriptor over the output when
+      // it spans at most 2 GiB, else through 64-bit addresses.
+      const bool whole = (uint64_t)P.M * (uint64_t)P.ldc * 2u <= 0x7fffffffull;
+      const OutWin wd = {make_rsrc(KIND == KIND_NT ? P.cout : P.c0, (uint64_t)P.M * P.ldc * 2), w.rowb};
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const uint4 v = staged(stage, wave, q * 4 + rq, cc);
+        if (!(KIND == KIND_NN && mapped)) win_store(w, voff, q * 4, v);
+        const int32_t d = mapped ? __shfl(tok2[round], q * 4 + rq, 64) : -1;
+        const float wq = KIND == KIND_NT && mapped ? bf16_to_f32((uint32_t)__shfl((int32_t)wt2[round], q * 4 + rq, 64)) : 0.f;
+        if ((KIND == KIND_NT || KIND == KIND_NN) && mapped && whole) {
+          const uint32_t vd = col < P.N && (uint32_t)d < (uint32_t)P.M ? (uint32_t)d * wd.rowb + (uint32_t)col * 2u : kOOB;
+          if (KIND == KIND_NN) {
+            win_store(wd, vd, 0, v);
+          } else {
+            float f[8];
+            unpack8(v, f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = __builtin_fmaf(f[e], wq, 0.f);
+            win_store(wd, vd, 0, pack8(f));
+          }
+        } else if ((KIND == KIND_NT || KIND == KIND_NN) && mapped && col < P.N && (uint32_t)d < (uint32_t)P.M) {
+          if (KIND == KIND_NN) {
+            st_stream(P.c0 + (int64_t)d * P.ldc + col, v);
+          } else {
+            // the combine kernel's rounding: 0 + bf16(f * w), as fma(f, w, 0)
+            float f[8];
+            unpack8(v, f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = __builtin_fmaf(f[e], wq, 0.f);
+            st_stream(P.cout + (int64_t)d * P.ldc + col, pack8(f));
+          }
+        }
+        if (q % 8 == 7) __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // Keep each round's loads and stores in their round (register pressure).
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// BAL (weight gradient): the balanced band order (build_wgrad_order); the
+// host picks it when the grid is 8 XCDs x 32 blocks and G <= NT.
+template <int KIND, bool BAL = false>
+__global__ __launch_bounds__(NT, 1) void grouped_gemm_w4_kernel(GemmParams P) {
+  static_assert(!BAL || KIND == KIND_TN, "the balanced order is the weight gradient's");
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE_BYTES];
+  __shared__ int32_t tpre[kMaxGroups + 1];
+  __shared__ int32_t scan_buf[NT];
+  __shared__ int4 ttab[kTileTab];
+  const int t = threadIdx.x;
+  const int wave = uni(t >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int G = P.G;
+
+  const int64_t grid = gridDim.x;
+  const int32_t xcd = (int32_t)(blockIdx.x % kNumXcd);
+  const int32_t xj = (int32_t)(blockIdx.x / kNumXcd);
+  int64_t ntn, tiles_per_group = 0, total;
+  int32_t deal_rounds = 0;
+  if constexpr (KIND == KIND_TN) {
+    const int64_t mtn = (P.M + BM - 1) / BM;
+    ntn = (P.N + BN - 1) / BN;
+    tiles_per_group = mtn * ntn;
+    total = tiles_per_group * G;
+    if constexpr (BAL) {
+      deal_rounds = uni(build_wgrad_order<NT>(P, tpre, scan_buf, t, total, tiles_per_group, xcd,
+                                              reinterpret_cast<int32_t*>(lds), (int32_t)(sizeof(lds) / sizeof(int32_t))));
+    }
+  } else {
+    ntn = (KIND == KIND_FC1) ? (P.I + 127) / 128 : (P.N + BN - 1) / BN;
+    group_prefix<BM, NT>(P, tpre, scan_buf, t);
+    total = (int64_t)tpre[G] * ntn;
+  }
+  int64_t slot = blockIdx.x;
+  if ((grid & 7) == 0) slot = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
+  const unsigned char* deal = reinterpret_cast<const unsigned char*>(tpre + G);
+
+  // The block's first kTileTab tiles, decoded at once into LDS (see grouped_gemm_kernel).
+  const int64_t rounds = (total + grid - 1) / grid;
+  const int32_t ntab = (int32_t)(rounds < kTileTab ? rounds : kTileTab);
+  const int32_t nk_all = KIND == KIND_TN ? 0 : (int32_t)((P.K + BK - 1) / BK);
+  for (int e = t; e < ntab; e += NT) {
+    TileInfo d;
+    bool ok;
+    if constexpr (!BAL) {
+      const int64_t tile = slot + (int64_t)e * grid;
+      ok = tile < total;
+      if (ok) d = decode_tile<KIND, BM, false>(P, tile, tpre, G, ntn, tiles_per_group);
+    } else {
+      const int32_t x = e < deal_rounds ? (int32_t)deal[e] : ((e & 1) ? kNumXcd - 1 - xcd : xcd);
+      const int64_t tile = ((int64_t)e * kNumXcd + x) * kBandTiles + xj;
+      ok = tile < total;
+      if (ok) {
+        const int64_t rank = tile / tiles_per_group;
+        d = decode_tile<KIND, BM, false>(P, scan_buf[rank], tpre, G, ntn, tiles_per_group, tile - rank * tiles_per_group);
+      }
+    }
+    ttab[e] = ok ? make_int4(d.row0, d.row_end, d.g | (d.ntile << 12), d.mtile) : make_int4(0, 0, 0, -1);
+  }
+  __syncthreads();
+
+  auto tile_at = [&](int64_t seq, TileInfo& ti) -> bool {
+    if (seq < ntab) {
+      const int4 e = ttab[seq];
+      if (uni(e.w) < 0) return false;
+      ti.row0 = uni(e.x);
+      ti.row_end = uni(e.y);
+      ti.g = uni(e.z) & 0xfff;
+      ti.ntile = uni(e.z) >> 12;
+      ti.mtile = uni(e.w);
+      ti.nk = KIND == KIND_TN ? (int32_t)(((int64_t)ti.row_end - ti.row0 + BK - 1) / BK) : nk_all;
+      return true;
+    }
+    if constexpr (!BAL) {
+      const int64_t tile = slot + seq * grid;
+      if (tile >= total) return false;
+      ti = decode_tile<KIND, BM>(P, tile, tpre, G, ntn, tiles_per_group);
+      return true;
+    } else {
+      const int32_t x = seq < deal_rounds ? uni((int32_t)deal[seq]) : ((seq & 1) ? kNumXcd - 1 - xcd : xcd);
+      const int64_t tile = (seq * kNumXcd + x) * kBandTiles + xj;
+      if (tile >= total) return false;
+      const int64_t rank = tile / tiles_per_group;
+      ti = decode_tile<KIND, BM>(P, uni(scan_buf[rank]), tpre, G, ntn, tiles_per_group, tile - rank * tiles_per_group);
+      return true;
+    }
+  };
+
+  // Consume cursor: the output tile being multiplied; tiles without K-tiles
+  // (weight gradient of an empty group) are written as zeros on the way.
+  int64_t c_seq = 0;
+  TileInfo cur;
+  for (;; ++c_seq) {
+    if (!tile_at(c_seq, cur)) return;
+    if (cur.nk > 0) break;
+    zero_tile<BM, NT>(P, cur, t);
+  }
+
+  // Issue cursor: the stream K-tile whose loads go out next.  Past the
+  // block's last K-tile it keeps its last tile with kt = 0, so those slots
+  // re-load that tile's first K-tile (in bounds, never multiplied).
+  Tile<KIND> it;
+  int64_t i_seq = c_seq;
+  int32_t i_kt = 0;
+  bool i_live = true;
+  it.i = cur;
+  setup<KIND>(P, it, wave, lane_id());
+  auto advance_issue = [&]() {
+    if (!i_live) return;
+    if (++i_kt < it.i.nk) return;
+    i_kt = 0;
+    while (tile_at(++i_seq, it.i)) {
+      if (it.i.nk > 0) {
+        setup<KIND>(P, it, wave, lane_id());
+        return;
+      }
+    }
+    i_live = false;
+  };
+
+  // Prologue: stream K-tiles 0 and 1 into the two stages; wait for the first.
+  static_for<0, 2 * QO>([&](auto j) __attribute__((always_inline)) {
+    issue<KIND, decltype(j)::value>(lds, it, i_kt, wave);
+  });
+  advance_issue();
+  static_for<0, 2 * QO>([&](auto j) __attribute__((always_inline)) {
+    issue<KIND, decltype(j)::value>(lds + STAGE_BYTES, it, i_kt, wave);
+  });
+  advance_issue();
+  wait_loads<2 * QO>();
+  block_barrier();
+  int cs = 0;  // stage of the K-tile being multiplied
+  f32x4_t acc[FM][FN];
+  Frags f0, f1;
+  {
+    const TileSlots<KIND> ts = tile_slots<KIND>(wm, wn, lane_id());
+    static_for<0, FM + FN>([&](auto j) __attribute__((always_inline)) {
+      read_frag<KIND, frag_order(decltype(j)::value)>(lds, 0, wm, wn, ts, f0);
+    });
+  }
+
+  // One k-step of MFMAs from `fm` (16 groups of 4), with the reads of k-step
+  // KS of `stage` into `fr` and, with LOADS, load J0 + j of the next stream
+  // K-tile into `refill` in the first 8 groups.
+  // `ts` holds the wave's fragment offsets, computed once per tile from the
+  // lane index passed through an opaque move, so that they are not hoisted
+  // out of the tile loop, where they would hold registers during the epilogue.
+  auto kstep = [&](auto ks, auto first, auto loads, auto j0, const char* stage, char* refill, const Frags& fm,
+                   Frags& fr, const TileSlots<KIND>& ts) __attribute__((always_inline)) {
+    static_for<0, 16>([&](auto jj) __attribute__((always_inline)) {
+      constexpr int j = decltype(jj)::value;
+      if constexpr (decltype(loads)::value == 2) issue<KIND, j>(refill, it, i_kt, wave);
+      else if constexpr (decltype(loads)::value == 1 && j < QO) issue<KIND, decltype(j0)::value + j>(refill, it, i_kt, wave);
+      if constexpr (decltype(ks)::value >= 0) read_frag<KIND, frag_order(j)>(stage, decltype(ks)::value, wm, wn, ts, fr);
+      mfma<4 * j, 4, decltype(first)::value>(fm, acc);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  for (;;) {
+    // Output tile `cur`.  Its first K-tile is in stage cs with k-step 0 in
+    // f0; the next stream K-tile is in flight into the other stage.
+    int ln = lane_id();
+    asm volatile("" : "+v"(ln));
+    const TileSlots<KIND> ts = tile_slots<KIND>(wm, wn, ln);
+    kstep(Int<1>{}, Int<1>{}, Int<0>{}, Int<0>{}, lds + cs * STAGE_BYTES, nullptr, f0, f1, ts);
+    wait_loads_lds<0>();
+    block_barrier();
+    cs ^= 1;
+    for (int32_t kt = 1; kt < cur.nk; ++kt) {
+      const char* stage = lds + cs * STAGE_BYTES;
+      char* refill = lds + (cs ^ 1) * STAGE_BYTES;
+      if constexpr ((PMX_W4_LOADS_FIRST_HALF >> KIND) & 1) {
+        // all of the next K-tile's loads among the first k-step's MFMAs
+        kstep(Int<0>{}, Int<0>{}, Int<2>{}, Int<0>{}, stage, refill, f1, f0, ts);
+        kstep(Int<1>{}, Int<0>{}, Int<0>{}, Int<0>{}, stage, refill, f0, f1, ts);
+      } else {
+        // half of them in each k-step
+        kstep(Int<0>{}, Int<0>{}, Int<1>{}, Int<0>{}, stage, refill, f1, f0, ts);
+        kstep(Int<1>{}, Int<0>{}, Int<1>{}, Int<QO>{}, stage, refill, f0, f1, ts);
+      }
+      advance_issue();
+      wait_loads_lds<0>();
+      block_barrier();
+      cs ^= 1;
+    }
+    // The tile's last k-step is in f1; stage cs holds the next stream
+    // K-tile (published by the barrier) and stage cs ^ 1 is free.
+    const TileInfo done = cur;
+    bool more = false;
+    while (tile_at(++c_seq, cur)) {
+      if (cur.nk > 0) {
+        more = true;
+        break;
+      }
+      zero_tile<BM, NT>(P, cur, t);
+    }
+    mfma<0, FM * FN>(f1, acc);
+    epilogue<KIND>(P, done, wm, wn, wave, lane_id(), acc, lds + (cs ^ 1) * STAGE_BYTES);
+    if (!more) {
+      wait_loads<0>();
+      return;
+    }
+    // Once this wave's staging reads have returned, the next stream K-tile
+    // goes into its chunks of the freed stage; then the next tile's first
+    // k-step is read (after the epilogue, so that its 64 registers are free
+    // during it).
+    wait_lds();
+    static_for<0, 2 * QO>([&](auto j) __attribute__((always_inline)) {
+      issue<KIND, decltype(j)::value>(lds + (cs ^ 1) * STAGE_BYTES, it, i_kt, wave);
+    });
+    advance_issue();
+    int ln2 = lane_id();
+    asm volatile("" : "+v"(ln2));
+    const TileSlots<KIND> ts2 = tile_slots<KIND>(wm, wn, ln2);
+    static_for<0, FM + FN>([&](auto j) __attribute__((always_inline)) {
+      read_frag<KIND, frag_order(decltype(j)::value)>(lds + cs * STAGE_BYTES, 0, wm, wn, ts2, f0);
+    });
+  }
+}
+
+}  // namespace w4
+
 // Buffer offsets are 32-bit: one descriptor covers at most 2 GiB.
 bool fits_rsrc(int64_t rows, int64_t ld) { return rows * ld * 2 < (int64_t)0x7fffffff; }
 
@@ -1403,6 +2128,25 @@ int grid_size() {
 constexpr int kBM = 256;
 constexpr int64_t kRsMaxRowsPerCopy = 8 * kBM;
 
+// The four-wave kernel takes the calls of the kinds in PMX_W4_KINDS (bit
+// KIND) whose loads can be FAST: fc1 + SwiGLU, fc2 dgrad + SwiGLU backward and
+// the weight gradients, where it measured faster in the layer (config 3: fc1
+// 3.02-3.05 vs 3.05 ms, fc2 dgrad 1.74-1.76 vs 1.73, fc2 wgrad 1.43 vs 1.48,
+// fc1 wgrad 2.89-2.90 vs 2.93; Qwen3 shape: 0.81 vs 0.84, 0.49-0.50 vs 0.51,
+// 0.46 vs 0.47, 0.78-0.79 vs 0.83).  The fc2 forward and the fc1 dgrad stay on
+// the eight-wave kernel's register-staged loads, faster there (config 3: 1.65
+// vs 1.67-1.68 and 3.06 vs 3.12-3.13; Qwen3 shape: 0.46 vs 0.50-0.51 and 0.80
+// vs 0.85-0.86).  PMX_GEMM_W4=0 builds the eight-wave kernel for every call
+// (the `w8` test variant, for comparisons).
+#ifndef PMX_GEMM_W4
+#define PMX_GEMM_W4 1
+#endif
+#ifndef PMX_W4_KINDS
+#define PMX_W4_KINDS ((1 << KIND_FC1) | (1 << KIND_NNS) | (1 << KIND_TN))
+#endif
+template <int KIND>
+constexpr bool use_w4() { return PMX_GEMM_W4 && ((PMX_W4_KINDS >> KIND) & 1); }
+
 template <int KIND>
 int launch(const GemmParams& P, hipStream_t stream) {
   // The LDS tile table keeps an n-tile index in 19 bits.
@@ -1413,6 +2157,17 @@ int launch(const GemmParams& P, hipStream_t stream) {
   if constexpr (KIND == KIND_TN) {
     // FAST: every row of both operands within 31-bit offsets (P.K = their rows).
     const bool fast = fits_rsrc(P.K, P.M) && fits_rsrc(P.K, P.N);
+    if constexpr (use_w4<KIND_TN>()) {
+      if (fast && fits_rsrc(P.M, P.N)) {
+        if (grid == kNumXcd * kBandTiles && P.G <= w4::NT) {
+          w4::grouped_gemm_w4_kernel<KIND_TN, true><<<grid, w4::NT, 0, stream>>>(P);
+        } else {
+          w4::grouped_gemm_w4_kernel<KIND_TN><<<grid, w4::NT, 0, stream>>>(P);
+        }
+        PMX_LAUNCH_CHECK();
+        return PMX_OK;
+      }
+    }
     const bool bal = grid == kNumXcd * kBandTiles && P.G <= NTHREADS;
     if (bal && fast) {
       grouped_gemm_kernel<KIND_TN, kBM, true, true><<<grid, NTHREADS, 0, stream>>>(P);
@@ -1430,6 +2185,13 @@ int launch(const GemmParams& P, hipStream_t stream) {
     // weight strip serves few tiles and its loads wait on memory - with a
     // few large copies the DMA path is faster (it spends less power).
     const bool fast = P.K % BK == 0 && (KIND != KIND_NN || P.b.split >= P.K);
+    if constexpr (use_w4<KIND>()) {
+      if (fast) {
+        w4::grouped_gemm_w4_kernel<KIND><<<grid, w4::NT, 0, stream>>>(P);
+        PMX_LAUNCH_CHECK();
+        return PMX_OK;
+      }
+    }
     if (!fast) {
       grouped_gemm_kernel<KIND, kBM><<<grid, NTHREADS, 0, stream>>>(P);
     } else if constexpr (KIND == KIND_FC1 || KIND == KIND_NT) {

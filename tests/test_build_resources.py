@@ -74,7 +74,8 @@ def test_planted_scratch_kernel_is_caught(tmp_path):
 @pytest.mark.parametrize("extra", [(), ("-DPMX_TILE_TAB=2",)], ids=["shipped", "tiletab2"])
 def test_shipped_gemm_kernels_have_no_scratch(extra, tmp_path):
     recs = _compile_remarks(build.CSRC / "grouped_gemm.hip", tmp_path, extra)
-    gemm = [r for r in recs if "grouped_gemm_kernel" in r["name"]]
-    assert len(gemm) >= 13, [r["name"] for r in recs]
+    gemm = [r for r in recs if "grouped_gemm" in r["name"]]
+    assert sum("grouped_gemm_kernel" in r["name"] for r in gemm) >= 13, [r["name"] for r in recs]
+    assert sum("grouped_gemm_w4_kernel" in r["name"] for r in gemm) >= 4, [r["name"] for r in recs]
     build.check_no_scratch(recs, build.RESOURCE_CHECKED["grouped_gemm.hip"], "grouped_gemm.hip")
     assert all(r["scratch"] == 0 and r["vgpr_spill"] == 0 for r in gemm)
