@@ -63,6 +63,7 @@ STAGES = [
     ("pmx_group_gemm_nt_combine_top1", 0, "fc2_fwd"),
     ("pmx_combine_fwd", 0, "combine_fwd"),
     ("pmx_combine_bwd", 0, "combine_bwd"),
+    ("pmx_combine_bwd_top1_rows", 0, "combine_bwd"),
     ("pmx_gemm_fc2_dgrad_swiglu_bwd", 0, "fc2_dgrad"),
     ("pmx_group_gemm_tn", 0, "fc2_wgrad"),
     ("pmx_group_gemm_tn", 1, "fc1_wgrad"),

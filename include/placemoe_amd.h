@@ -133,6 +133,20 @@ int pmx_combine_fwd(const void* Y, const int32_t* pos, const void* w, int64_t T,
 int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const void* w,
                     int64_t T, int32_t K, int64_t H, void* dY, void* dw, pmx_stream_t stream);
 
+/* Top-1 routing only (K = 1): pmx_combine_bwd walked in the rows' storage
+ * order.  Row r of Y and dY belongs to token row_token[r] (the row map that
+ * pmx_moe_scatter_src writes), so Y is read and dY written front to back and
+ * only dout is gathered:
+ *   dY[r]            = bf16(dout[row_token[r]] * w[row_token[r]])
+ *   dw[row_token[r]] = bf16( sum_h fp32( bf16(dout[row_token[r],h] * Y[r,h]) ) )
+ * Bit-identical to pmx_combine_bwd(dout, Y, pos, w, T, 1, H, dY, dw) when
+ * row_token is the row map of pos.  A row whose row_token lies outside
+ * [0, T) gets dY[r] = 0 and writes no dw.  H must be a multiple of 8 and
+ * dout, Y, dY 16-byte aligned (PMX_ERR_SHAPE otherwise).  Replaces the same
+ * reference code as pmx_combine_bwd (all_to_all.py:2552, :930-933). */
+int pmx_combine_bwd_top1_rows(const void* dout, const void* Y, const int32_t* row_token, const void* w,
+                              int64_t T, int64_t H, void* dY, void* dw, pmx_stream_t stream);
+
 /* Bytes of workspace pmx_segment_sum needs. */
 size_t pmx_segment_sum_workspace_bytes(int64_t num_src_rows, int64_t num_rows);
 

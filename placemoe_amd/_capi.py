@@ -52,6 +52,10 @@ SIGNATURES = {
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_int64, c_void_p, c_void_p, c_void_p],
     ),
+    "pmx_combine_bwd_top1_rows": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p],
+    ),
     "pmx_segment_sum_workspace_bytes": (c_size_t, [c_int64, c_int64]),
     "pmx_segment_sum": (
         c_int,

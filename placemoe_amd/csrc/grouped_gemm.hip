@@ -1708,6 +1708,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
   // those of rows l and 64 + l, and a store's lanes fetch theirs with a
   // cross-lane read.  Targets outside [0, M) are not written.
   const bool mapped = (KIND == KIND_NT || KIND == KIND_NN) && P.row_tok != nullptr;
+  uint4 nns_g[KIND == KIND_NNS ? 2 : 1][4], nns_u[KIND == KIND_NNS ? 2 : 1][4];  // KIND_NNS: two quarters of gate/up
   int32_t tok2[2] = {-1, -1};
   uint32_t wt2[2] = {0, 0};
   if constexpr (KIND == KIND_NT || KIND == KIND_NN) {
@@ -1775,37 +1776,50 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
     } else if constexpr (KIND == KIND_NNS) {
       // fc2 dgrad: the tile is dact (bf16, as the reference stores it) for
       // columns j < I; with the forward's gate/up of the same rows it becomes
-      // [d_gate | d_up] of dG1.  Each half round's gate/up loads go out before
-      // its staging reads.
+      // [d_gate | d_up] of dG1.  The rows go in quarters of 16 (4 stores of
+      // each half); each quarter's gate/up loads are issued a quarter ahead,
+      // so that waiting for them does not also wait for the previous
+      // quarter's stores (one counter tracks a wave's loads and stores in
+      // issue order).  The next round's first loads go out during this
+      // round's last quarter.
       const int64_t I = P.I;
       const int64_t j = (int64_t)ti.ntile * BN + wn * 128 + cc * 8;
-      const OutWin wi = out_window(P.gin, ti.row0 + rb, ti.row_end, 2 * I);
-      const OutWin wo = out_window(P.c0, ti.row0 + rb, ti.row_end, 2 * I);
-      const uint32_t vg = j < I ? (uint32_t)rq * wi.rowb + (uint32_t)j * 2u : kOOB;
+      const uint32_t vg = j < I ? (uint32_t)rq * (uint32_t)(4 * I) + (uint32_t)j * 2u : kOOB;  // row rq of a quarter
       const uint32_t vu = vg + (uint32_t)I * 2u;
+      // gate/up rows of quarter qq (0..7 over both rounds) of the wave's 128 rows
+      auto window = [&](int qq) {
+        return out_window(P.gin, ti.row0 + wm * 128 + (qq >> 2) * 64, ti.row_end, 2 * I);
+      };
+      auto load_q = [&](int qq, uint4 (&gv)[4], uint4 (&uv)[4]) __attribute__((always_inline)) {
+        const OutWin wi = window(qq);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = (qq & 3) * 16 + q * 4;  // first row of the store within the round
+          gv[q] = win_load(wi, vg, r);
+          uv[q] = win_load(wi, vu, r);
+        }
+      };
+      if (round == 0) load_q(0, nns_g[0], nns_u[0]);
       stage_round<FN>(stage, wave, lane, round, [&](int mt, int nt) { return bf16x4(acc[mt][nt]); },
                       [](int nt) { return nt; });
+      const OutWin wo = out_window(P.c0, ti.row0 + rb, ti.row_end, 2 * I);
 #pragma unroll
-      for (int hr = 0; hr < 2; ++hr) {
-        uint4 gv[8], uv[8];
+      for (int qr = 0; qr < 4; ++qr) {
+        const int qq = round * 4 + qr;
+        if (qq < 7) load_q(qq + 1, nns_g[(qq + 1) & 1], nns_u[(qq + 1) & 1]);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          gv[q] = win_load(wi, vg, (hr * 8 + q) * 4);
-          uv[q] = win_load(wi, vu, (hr * 8 + q) * 4);
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int r = (hr * 8 + q) * 4;
+        for (int q = 0; q < 4; ++q) {
+          const int r = qr * 16 + q * 4;
           const uint4 v = staged(stage, wave, r + rq, cc);
           float d[8], g[8], u[8], dg[8], du[8];
           unpack8(v, d);
-          unpack8(gv[q], g);
-          unpack8(uv[q], u);
+          unpack8(nns_g[qq & 1][q], g);
+          unpack8(nns_u[qq & 1][q], u);
           swiglu_bwd8(d, g, u, dg, du);
           win_store(wo, vg, r, pack8(dg));
           win_store(wo, vu, r, pack8(du));
         }
-        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
       }
     } else if constexpr (KIND == KIND_TN) {
       // Rows m of copy g's gradient: those below csplit in c0, the rest in

@@ -219,6 +219,25 @@ def combine_bwd(dout: torch.Tensor, y: torch.Tensor, pos: torch.Tensor, w: torch
     return dy, dw
 
 
+def combine_bwd_top1_rows(dout: torch.Tensor, y: torch.Tensor, row_token: torch.Tensor, w: torch.Tensor):
+    """Top-1 combine gradient walked in the rows' storage order (row_token:
+    the row map of moe_scatter_src) -> (dY [T, H], dw [T, 1]); bit-identical
+    to combine_bwd with the matching pos."""
+    dev = _check_dev(dout, y, row_token, w)
+    _bf16("dout", dout)
+    _bf16("y", y)
+    _bf16("routing weights", w)
+    T, H = dout.shape
+    assert y.shape == (T, H), "top-1: one row of Y per token"
+    assert row_token.dtype == torch.int32 and row_token.is_contiguous() and row_token.numel() == T
+    assert w.numel() == T, "top-1 routing weights: one per token"
+    dy = torch.empty((T, H), dtype=y.dtype, device=dev)
+    dw = torch.empty((T, 1), dtype=w.dtype, device=dev)
+    _capi.call("pmx_combine_bwd_top1_rows", _ptr(dout), _ptr(y), _ptr(row_token), _ptr(w), T, H, _ptr(dy), _ptr(dw),
+               _stream(dev))
+    return dy, dw
+
+
 def segment_sum(source: torch.Tensor, index: torch.Tensor, num_rows: int) -> torch.Tensor:
     """out[r] = sum_{i: index[i]==r} source[i] in fp32, stored as bf16.
 

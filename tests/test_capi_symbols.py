@@ -68,6 +68,11 @@ def test_argument_errors_are_codes_not_crashes():
     assert lib.pmx_group_gemm_nt(None, None, None, 0, 8, 8, 8, None, None) == _capi.PMX_ERR_ARG
     assert lib.pmx_group_gemm_nt(None, None, None, 4, 8, 12, 8, None, None) == _capi.PMX_ERR_SHAPE
     assert lib.pmx_combine_bwd(None, None, None, None, 4, 33, 8, None, None, None) == _capi.PMX_ERR_ARG
+    dummy = ctypes.c_void_p(16)
+    assert lib.pmx_combine_bwd_top1_rows(None, None, None, None, 4, 8, None, None, None) == _capi.PMX_ERR_ARG
+    assert lib.pmx_combine_bwd_top1_rows(dummy, dummy, dummy, dummy, -1, 8, dummy, dummy, None) == _capi.PMX_ERR_ARG
+    assert lib.pmx_combine_bwd_top1_rows(dummy, dummy, dummy, dummy, 4, 12, dummy, dummy, None) == _capi.PMX_ERR_SHAPE
+    assert lib.pmx_combine_bwd_top1_rows(dummy, dummy, dummy, dummy, 0, 8, dummy, dummy, None) == _capi.PMX_OK
     with pytest.raises(ValueError):
         _capi.call("pmx_group_gemm_nt", None, None, None, 4, 8, 12, 8, None, None)
 

@@ -1,7 +1,8 @@
 """Top-1 epilogue fusions: the router-weighted combine inside the fc2 GEMM
 and the unpermute gradient inside the fc1 dgrad are bit-identical to the
 separate kernels they replace (and a top-1 layer with them to the layer
-without them); the scatter's row-source map is the inverse of the scatter
+without them); the combine gradient walked in row order equals the
+token-order one; the scatter's row-source map is the inverse of the scatter
 index; row targets outside the output are never written."""
 
 import numpy as np
@@ -56,6 +57,45 @@ def test_scatter_row_source_inverts_pos(cuda, K):
     assert none is None
     assert_exact(xp2, xp, "rows without weights")
     assert_exact(src2, src, "row sources without weights")
+
+
+@pytest.mark.parametrize("T,H", [(1000, 64), (777, 7168), (3000, 2048), (5, 8), (4096, 4104), (300, 14336)])
+def test_combine_bwd_top1_rows_matches_token_order(cuda, T, H):
+    pos, inv = _perm(T, 70 + T, cuda)
+    g = torch.Generator(device=cuda).manual_seed(H)
+    dout = torch.randn((T, H), generator=g, device=cuda).to(torch.bfloat16)
+    y = torch.randn((T, H), generator=g, device=cuda).to(torch.bfloat16)
+    w = torch.rand((T, 1), generator=g, device=cuda).to(torch.bfloat16)
+    print(f"combine gradient row order: T={T} H={H}", flush=True)
+    dy, dw = kernels.combine_bwd(dout, y, pos, w)
+    dy2, dw2 = kernels.combine_bwd_top1_rows(dout, y, inv, w)
+    assert_exact(dy2, dy, "dY")
+    assert_exact(dw2, dw, "dw")
+
+
+def test_combine_bwd_top1_rows_skips_invalid_row_tokens(cuda):
+    T, H = 64, 128
+    pos, inv = _perm(T, 5, cuda)
+    g = torch.Generator(device=cuda).manual_seed(6)
+    dout = torch.randn((T, H), generator=g, device=cuda).to(torch.bfloat16)
+    y = torch.randn((T, H), generator=g, device=cuda).to(torch.bfloat16)
+    w = torch.rand((T, 1), generator=g, device=cuda).to(torch.bfloat16)
+    dy_ref, dw_ref = kernels.combine_bwd(dout, y, pos, w)
+    bad = inv.clone()
+    lost = [int(inv[3]), int(inv[7])]
+    bad[3], bad[7] = -1, T
+    dy = torch.full((T, H), 7.0, device=cuda, dtype=torch.bfloat16)
+    dw = torch.full((T, 1), 9.0, device=cuda, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream().cuda_stream
+    _capi.call("pmx_combine_bwd_top1_rows", dout.data_ptr(), y.data_ptr(), bad.data_ptr(), w.data_ptr(), T, H,
+               dy.data_ptr(), dw.data_ptr(), stream)
+    torch.cuda.synchronize()
+    keep = [r for r in range(T) if r not in (3, 7)]
+    assert_exact(dy[keep], dy_ref[keep], "dY of valid rows")
+    assert torch.count_nonzero(dy[[3, 7]]) == 0, "rows with an invalid token must be zero"
+    ok = [t for t in range(T) if t not in lost]
+    assert_exact(dw[ok], dw_ref[ok], "dw of tokens with a valid row")
+    assert torch.all(dw[lost] == 9.0), "tokens whose row is invalid keep their dw"
 
 
 @pytest.mark.parametrize("groups", list(GROUPS))
