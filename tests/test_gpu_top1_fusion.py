@@ -59,6 +59,22 @@ def test_scatter_row_source_inverts_pos(cuda, K):
     assert_exact(src2, src, "row sources without weights")
 
 
+@pytest.mark.parametrize("T,H", [(1000, 64), (777, 7168), (3000, 2048), (5, 8), (4096, 4104)])
+def test_top1_permute_in_row_order_matches_token_order(cuda, T, H):
+    """With the row map requested, the top-1 permute copies rows in their
+    storage order; without it, in token order: the rows must agree."""
+    pos, inv = _perm(T, 90 + T, cuda)
+    g = torch.Generator(device=cuda).manual_seed(T)
+    x = torch.randn((T, H), generator=g, device=cuda).to(torch.bfloat16)
+    w = torch.rand((T, 1), generator=g, device=cuda).to(torch.bfloat16)
+    print(f"permute row order: T={T} H={H}", flush=True)
+    xp_token = kernels.moe_scatter(x, pos)
+    xp_row, src, row_w = kernels.moe_scatter_src(x, pos, w)
+    assert_exact(xp_row, xp_token, "rows")
+    assert_exact(src, inv, "row map")
+    assert_exact(row_w, w.reshape(-1)[inv.long()], "row weights")
+
+
 @pytest.mark.parametrize("T,H", [(1000, 64), (777, 7168), (3000, 2048), (5, 8), (4096, 4104), (300, 14336)])
 def test_combine_bwd_top1_rows_matches_token_order(cuda, T, H):
     pos, inv = _perm(T, 70 + T, cuda)
