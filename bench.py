@@ -44,12 +44,12 @@ PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 # cannot be read from inside a timed run, so the figure is carried here; other
 # workloads report traffic null.
 MEASURED_TRAFFIC_BYTES = {
-    ("dsv3", "fc1_fwd"): (6159 + 954) * 2**20,
-    ("dsv3", "fc1_wgrad"): (5838 + 896) * 2**20,
-    ("dsv3", "fc1_dgrad"): (6923 + 896) * 2**20,
-    ("qwen3", "fc1_fwd"): (2444 + 727) * 2**20,
-    ("qwen3", "fc1_wgrad"): (1349 + 960) * 2**20,
-    ("qwen3", "fc1_dgrad"): (2081 + 512) * 2**20,
+    ("dsv3", "fc1_fwd"): (7384 + 769) * 2**20,
+    ("dsv3", "fc1_wgrad"): (8868 + 896) * 2**20,
+    ("dsv3", "fc1_dgrad"): (6765 + 896) * 2**20,
+    ("qwen3", "fc1_fwd"): (2444 + 576) * 2**20,
+    ("qwen3", "fc1_wgrad"): (1349 + 961) * 2**20,
+    ("qwen3", "fc1_dgrad"): (2083 + 512) * 2**20,
 }
 
 # Entry-point call order inside one step; repeated names are told apart by

@@ -107,8 +107,9 @@ int pmx_moe_scatter(const void* X, const int32_t* pos, int64_t T, int32_t K, int
  * row_src).  With top-1 routing (K = 1) row_src[r] is the token of row r:
  * the row map of pmx_group_gemm_nt_combine_top1 and
  * pmx_group_gemm_nn_unpermute_top1; the call then writes the map first and
- * copies the rows in their storage order (a row that pos does not name is
- * set to zero; pos from pmx_route names every row).  Replaces moe_scatter (moe.py:299-333)
+ * copies the rows in their storage order (a row that pos does not name gets
+ * row_src -1 and a zero row, its row_w is left as it was; pos from pmx_route
+ * names every row).  Replaces moe_scatter (moe.py:299-333)
  * plus the inverse of the scatter index that moe_gather's backward reads
  * (moe.py:126-159). */
 int pmx_moe_scatter_src(const void* X, const int32_t* pos, const void* w, int64_t T, int32_t K,

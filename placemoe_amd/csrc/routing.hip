@@ -823,7 +823,10 @@ int pmx_moe_scatter_src(const void* X, const int32_t* pos, const void* w, int64_
   bf16_t* rw = static_cast<bf16_t*>(row_w);
   if (H % 8 == 0 && aligned16(X) && aligned16(Xp)) {
     if (K == 1 && row_src != nullptr) {
-      // top-1 with the row map: the map first, then the rows in storage order
+      // top-1 with the row map: the map first (every row -1, then the rows
+      // pos names), then the rows in storage order
+      fill_i32_kernel<<<(unsigned)((T + 255) / 256), 256, 0, stream>>>(row_src, T, -1);
+      PMX_LAUNCH_CHECK();
       invert_top1_kernel<<<(unsigned)((T + 255) / 256), 256, 0, stream>>>(pos, wb, T, row_src, rw);
       PMX_LAUNCH_CHECK();
       gather_rows_by_src_kernel<<<(unsigned)T, th, 0, stream>>>((const bf16_t*)X, row_src, T, H, (bf16_t*)Xp);

@@ -13,6 +13,12 @@
   (balanced for G <= 512 copies, plain beyond); its outputs must equal the
   shipped library's bit for bit (every tile is computed the same way wherever
   it is decoded) and the fp32 products within the bf16 bar.
+* The shipped library runs fc1 + SwiGLU, the fc2 dgrad and the weight
+  gradients on the four-wave kernel whenever K is a multiple of 64.  The test
+  build ``libplacemoe_amd_w8.so`` runs the eight-wave kernel for every call,
+  so its fast-load paths of those kinds stay covered: every kind against the
+  fp32 products, and the two builds within the bf16 bar of each other (their
+  MFMA shapes sum in different orders, so the bits may differ).
 """
 
 import numpy as np
@@ -94,3 +100,18 @@ def test_tile_table_overflow_path(cuda, G, A, H, I):
         for k in ref:
             assert torch.equal(got[k], ref[k]), f"{k}: the two-entry tile table changes the result"
         check_every_kind(cuda, off, H, I, 9, f"tiletab2 G={G}")
+
+
+@pytest.mark.parametrize("G,A,H,I", [(16, 20000, 1024, 512), (160, 30000, 512, 256), (5, 3000, 256, 192)],
+                         ids=["g16", "g160", "g5"])
+def test_eight_wave_build_every_kind(cuda, G, A, H, I):
+    variant = build.variant_path("w8")
+    assert variant.exists(), f"{variant} is not built (python -m placemoe_amd.build)"
+    off = _copies(G, A, seed=G + 7)
+    print(f"eight-wave build: G={G} A={int(off[-1])} H={H} I={I}", flush=True)
+    ref = _outputs(cuda, off, H, I, seed=6)
+    with _capi.using(variant):
+        got = _outputs(cuda, off, H, I, seed=6)
+        check_every_kind(cuda, off, H, I, 10, f"w8 G={G}")
+    for k in ref:
+        assert_bf16_close(got[k], ref[k], name=f"eight-wave against shipped build: {k}")

@@ -75,6 +75,32 @@ def test_top1_permute_in_row_order_matches_token_order(cuda, T, H):
     assert_exact(row_w, w.reshape(-1)[inv.long()], "row weights")
 
 
+def test_top1_permute_rows_not_named_by_pos(cuda):
+    """A pos that names some rows twice and some not at all (not what
+    pmx_route produces, but the entry point takes any pos): the unnamed rows
+    get row_src -1 and zeros, whatever the output buffers held before."""
+    T, H = 300, 256
+    pos, _ = _perm(T, 17, cuda)
+    pos[::7] = pos[1::7][: pos[::7].numel()]  # every 7th token lands on its neighbour's row
+    pos[5] = T + 3  # outside the rows: skipped
+    named = torch.zeros(T, dtype=torch.bool, device=cuda)
+    named[pos[(pos >= 0) & (pos < T)].long()] = True
+    g = torch.Generator(device=cuda).manual_seed(3)
+    x = torch.randn((T, H), generator=g, device=cuda).to(torch.bfloat16)
+    w = torch.rand((T, 1), generator=g, device=cuda).to(torch.bfloat16)
+    print(f"permute rows not named: T={T} H={H} unnamed={int((~named).sum())}", flush=True)
+    for _ in range(2):  # the second call gets recycled (non-zero) buffers from the allocator
+        xp, src, _ = kernels.moe_scatter_src(x, pos, w)
+        torch.cuda.synchronize()
+        assert int((~named).sum()) > 0
+        assert (src[~named] == -1).all(), "unnamed rows keep a stale row map entry"
+        assert (xp[~named] == 0).all(), "unnamed rows are not zero"
+        ok = named.nonzero().flatten()
+        assert_exact(xp[ok], x[src[ok].long()], "named rows")
+        assert (pos.view(-1)[src[ok].long()] == ok.to(pos.dtype)).all(), "row map does not invert pos"
+        del xp, src
+
+
 @pytest.mark.parametrize("T,H", [(1000, 64), (777, 7168), (3000, 2048), (5, 8), (4096, 4104), (300, 14336)])
 def test_combine_bwd_top1_rows_matches_token_order(cuda, T, H):
     pos, inv = _perm(T, 70 + T, cuda)
