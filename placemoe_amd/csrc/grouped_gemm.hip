@@ -847,9 +847,26 @@ __device__ __forceinline__ void zero_tile(const GemmParams& P, const TileInfo& t
 // (m fastest).  The 32 blocks of one XCD, which run consecutive tiles, then
 // cover 8 m-tiles x 4 n-tiles and share both operands through that XCD's L2:
 // 8 A + 4 B strips (128 KB per K-tile) instead of the 1-2 A + 16-28 B strips
-// of an n-fastest order over wide outputs.
-constexpr int64_t kBand = 8;
+// of an n-fastest order over wide outputs.  (PMX_BAND / PMX_BAND_TN: other
+// band heights, for measurements.)
+#ifndef PMX_BAND
+#define PMX_BAND 8
+#endif
+#ifndef PMX_BAND_TN
+#define PMX_BAND_TN PMX_BAND
+#endif
+#ifndef PMX_BAND_NNS
+#define PMX_BAND_NNS PMX_BAND
+#endif
+template <int KIND>
+constexpr int64_t band_height() {
+  return KIND == KIND_TN ? PMX_BAND_TN : KIND == KIND_NNS ? PMX_BAND_NNS : PMX_BAND;
+}
+static_assert(PMX_BAND >= 1 && PMX_BAND <= 32 && PMX_BAND_TN >= 1 && PMX_BAND_TN <= 32 && PMX_BAND_NNS >= 1 &&
+                  PMX_BAND_NNS <= 32,
+              "band height");
 
+template <int64_t kBand>
 __device__ __forceinline__ void band_order(int64_t t, int64_t mtiles, int64_t ntn, int64_t& m, int64_t& n) {
   const int64_t band = t / (kBand * ntn);
   const int64_t m0 = band * kBand;
@@ -877,14 +894,14 @@ __device__ __forceinline__ TileInfo decode_tile(const GemmParams& P, int64_t til
       g = tile / tiles_per_group;
       local = tile - g * tiles_per_group;
     }
-    band_order(local, tiles_per_group / ntn, ntn, m, n);
+    band_order<band_height<KIND>()>(local, tiles_per_group / ntn, ntn, m, n);
     ti.g = (int32_t)g;
     ti.mtile = (int32_t)m;
     ti.row0 = P.offsets[g];
     ti.row_end = P.offsets[g + 1];
     ti.nk = (int32_t)(((int64_t)ti.row_end - ti.row0 + BK - 1) / BK);
   } else {
-    band_order(tile, tpre[G], ntn, m, n);
+    band_order<band_height<KIND>()>(tile, tpre[G], ntn, m, n);
     // Uniform binary search for the group holding m-tile m.
     int lo = 0, hi = G;
     while (lo < hi) {
