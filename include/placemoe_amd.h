@@ -260,6 +260,30 @@ int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int3
                       int64_t c_copy_stride, int64_t c_split, pmx_stream_t stream);
 
 /* ------------------------------------------------------------------------ */
+/* Router weight on the fc2 input (the reference's non-EP arithmetic)        */
+/* ------------------------------------------------------------------------ */
+
+/* out[r] = bf16(act[r] * row_w[r]);  act, out [R,N] bf16, row_w bf16 [R]
+ * (each permuted row's router weight, as pmx_moe_scatter_src writes it).
+ * Replaces fc1_weighted_output = fc1_activation * scattered_gate_weight
+ * (veomni/ops/kernels/moe/group_gemm.py:269-276 split, :494-499 merged). */
+int pmx_weight_rows(const void* act, const void* row_w, int64_t R, int64_t N, void* out,
+                    pmx_stream_t stream);
+
+/* Backward of pmx_weight_rows fused with the SwiGLU backward, per row r:
+ *   dact          = bf16(d_act_w[r] * row_w[r])
+ *   dw[row_src[r]] = bf16( sum_j fp32( bf16(act[r,j] * d_act_w[r,j]) ) )
+ *   dG1[r]        = [ d_gate | d_up ] of dact with the rounding points of
+ *                   pmx_gemm_fc2_dgrad_swiglu_bwd (aten silu_backward)
+ * d_act_w, act [R,I], gu and dG1 [R,2I] (gate | up) bf16; row_src int32 [R]
+ * (the row's index t*K+k in dw [A] bf16; entries outside [0, A) write no dw;
+ * row_src and dw both NULL: no dw).  Replaces group_gemm.py:365-377 and :406
+ * (split), :577-592 (merged). */
+int pmx_swiglu_bwd_weighted(const void* d_act_w, const void* gu, const void* act, const void* row_w,
+                            const int32_t* row_src, int64_t R, int64_t I, int64_t A, void* dG1,
+                            void* dw, pmx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
 /* Replica-gradient fold                                                     */
 /* ------------------------------------------------------------------------ */
 

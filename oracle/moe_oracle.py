@@ -26,6 +26,13 @@ How each function is pinned (the checks live in ``tests/test_oracle_*.py``):
 * ``expert_layer_forward`` / ``expert_layer_backward`` - an independent
   float64 autograd model (the reference test's per-expert eager loop,
   tests/ops/test_fused_moe_split_vs_merged.py:21-44), forward and gradients.
+* ``row_weights`` / ``weight_rows`` / ``swiglu_backward_weighted`` /
+  ``moe_layer_forward_weighted_input`` / ``moe_layer_backward_weighted_input``
+  (the non-EP branch) - the same float64 autograd model (the router weight
+  commutes with fc2 in exact arithmetic); with power-of-two router weights,
+  where every product with the weight is exact, the output, dx, dw1 and dw2
+  equal the EP branch's bit for bit; a planted backward that drops the
+  router weight from dact is caught.
 * ``combine_forward`` / ``combine_backward`` / ``unpermute_grad`` - fp32
   ``index_add_`` (tests/distributed/test_hiermoe_cuda_combine.py:41-51),
   autograd of the weighted sum, and the reference's double-precision eager
@@ -362,6 +369,78 @@ def moe_layer_backward(dout, fwd, w, w1, w2):
     dxp, dw1, dw2, dg1 = expert_layer_backward(dy, fwd["xp"], fwd["gu"], fwd["offsets"], w1, w2)
     dx = unpermute_grad(dxp, fwd["pos"])
     return dict(dy=dy, dw=dw, dxp=dxp, dw1=dw1, dw2=dw2, dg1=dg1, dx=dx)
+
+
+# ---------------------------------------------------------------------------
+# Router weight on the fc2 input (the reference's non-EP branch)
+# ---------------------------------------------------------------------------
+
+
+def row_weights(w: torch.Tensor, pos) -> torch.Tensor:
+    """scattered_gate_weight[scatter_index.flatten()] = gate_weights.reshape(-1)
+    (veomni/ops/kernels/moe/group_gemm.py:269-272, :494-497): each permuted
+    row's router weight."""
+    pos_t = torch.as_tensor(np.asarray(pos, dtype=np.int64)).reshape(-1)
+    out = torch.empty(pos_t.numel(), dtype=w.dtype)
+    out[pos_t] = w.reshape(-1)
+    return out
+
+
+def weight_rows(act: torch.Tensor, row_w: torch.Tensor) -> torch.Tensor:
+    """fc1_weighted_output = fc1_activation * scattered_gate_weight, a bf16
+    product (group_gemm.py:276, :499)."""
+    return (act.float() * row_w.float()[:, None]).to(act.dtype)
+
+
+def swiglu_backward_weighted(d_act_w: torch.Tensor, gu: torch.Tensor, act: torch.Tensor, row_w: torch.Tensor):
+    """The router weight's backward and the SwiGLU backward of the non-EP
+    branch (group_gemm.py:577-592; split :365-406), returning (dg1 [R,2I],
+    dw_row [R]):
+    grad_fc1_activation = bf16(d_act_w * w), grad_scattered_gate_weight =
+    bf16(sum_j fp32(bf16(act * d_act_w))) (``torch.sum`` of a bf16 product),
+    then silu_backward and the up-projection product as in the EP branch."""
+    I = act.shape[1]
+    dact = (d_act_w.float() * row_w.float()[:, None]).to(BF16)
+    dw_row = (act.float() * d_act_w.float()).to(BF16).float().sum(dim=1).to(row_w.dtype)
+    d_gate, d_up = swiglu_backward(dact, gu[:, :I], gu[:, I:])
+    return torch.cat([d_gate, d_up], dim=1), dw_row
+
+
+def moe_layer_forward_weighted_input(x, w, phys, w1, w2):
+    """``MergedFc1TritonFusedMoeExpertFunction.forward`` (group_gemm.py:458-531)
+    for already-mapped ``phys``: the router weight multiplies the fc2 input and
+    ``moe_gather`` sums a token's rows unweighted."""
+    C = w1.shape[0]
+    counts = histogram(phys, C)
+    offsets = group_offsets(counts)
+    pos = scatter_index(phys)
+    xp = permute(x, pos)
+    gu = grouped_gemm_nt(xp, w1, offsets)
+    I = w1.shape[1] // 2
+    act = swiglu_forward(gu[:, :I], gu[:, I:])
+    row_w = row_weights(w, pos)
+    act_w = weight_rows(act, row_w)
+    y = grouped_gemm_nt(act_w, w2, offsets)
+    out = unpermute_grad(y, pos)
+    return dict(counts=counts, offsets=offsets, pos=pos, xp=xp, gu=gu, act=act, row_w=row_w, act_w=act_w, y=y,
+                out=out)
+
+
+def moe_layer_backward_weighted_input(dout, fwd, w, w1, w2):
+    """``MergedFc1TritonFusedMoeExpertFunction.backward`` (group_gemm.py:533-629):
+    grad_fc2_output = moe_scatter(grad_output), its dgrad through fc2, the
+    router weight's backward, fc1 as in the EP branch, ``moe_gather``."""
+    pos, offsets = fwd["pos"], fwd["offsets"]
+    dyp = permute(dout, pos)
+    d_act_w = grouped_gemm_nn(dyp, w2, offsets)
+    dw2 = grouped_gemm_tn(dyp, fwd["act_w"], offsets)
+    dg1, dw_row = swiglu_backward_weighted(d_act_w, fwd["gu"], fwd["act"], fwd["row_w"])
+    pos_t = torch.as_tensor(np.asarray(pos, dtype=np.int64)).reshape(-1)
+    dw = dw_row[pos_t].reshape(w.shape)
+    dxp = grouped_gemm_nn(dg1, w1, offsets)
+    dw1 = grouped_gemm_tn(dg1, fwd["xp"], offsets)
+    dx = unpermute_grad(dxp, pos)
+    return dict(dyp=dyp, d_act_w=d_act_w, dg1=dg1, dw_row=dw_row, dw=dw, dxp=dxp, dw1=dw1, dw2=dw2, dx=dx)
 
 
 # ---------------------------------------------------------------------------

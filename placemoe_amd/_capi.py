@@ -94,6 +94,12 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64,
          c_void_p],
     ),
+    "pmx_weight_rows": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "pmx_swiglu_bwd_weighted": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+         c_void_p],
+    ),
     "pmx_replica_fold": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, POINTER(c_float), c_int32,

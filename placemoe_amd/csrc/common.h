@@ -79,6 +79,31 @@ __device__ __forceinline__ void st_row(void* p, const uint4 v) {
 __device__ __forceinline__ float sigmoid_f32(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ float silu_f32(float x) { return x * sigmoid_f32(x); }
 
+// SwiGLU backward of 8 columns, with the reference's rounding points
+// (aten silu_backward and the products around it in
+// EPMergedFc1GroupGemm.backward, veomni/distributed/moe/moe_layer.py:453-482,
+// :479): dact is the bf16 dgrad output,
+//   s = bf16(silu(g)), d_silu = bf16(dact * u), sig = sigmoid(g)
+//   dgate = d_silu * sig * (1 + g * (1 - sig)),  dup = s * dact,
+// with sig * (1 + g * (1 - sig)) evaluated as sig + silu(g) * (1 - sig) in
+// one fma (fp32 rounding differs from aten's order by a few ulp).
+__device__ __forceinline__ void swiglu_bwd8(const float* dact, const float* g, const float* u, float* dgate,
+                                            float* dup) {
+#pragma unroll
+  for (int q = 0; q < 8; q += 2) {
+    const float sig0 = sigmoid_f32(g[q]), sig1 = sigmoid_f32(g[q + 1]);
+    const float gs0 = g[q] * sig0, gs1 = g[q + 1] * sig1;
+    float s0 = gs0, s1 = gs1;
+    float d0 = dact[q] * u[q], d1 = dact[q + 1] * u[q + 1];
+    round2_bf16(s0, s1);
+    round2_bf16(d0, d1);
+    dgate[q] = d0 * __builtin_fmaf(gs0, 1.0f - sig0, sig0);
+    dgate[q + 1] = d1 * __builtin_fmaf(gs1, 1.0f - sig1, sig1);
+    dup[q] = s0 * dact[q];
+    dup[q + 1] = s1 * dact[q + 1];
+  }
+}
+
 // Wave-wide sum (64 lanes) with cross-lane shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

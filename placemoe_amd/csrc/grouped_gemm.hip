@@ -465,31 +465,6 @@ __device__ __forceinline__ void static_for(F&& f) {
 // wave issues its next loads.  Rows of a round are 128 bytes; 16-byte chunk c
 // of row r sits at c ^ ((r >> 1) & 7).
 
-// SwiGLU backward of 8 columns, with the reference's rounding points
-// (aten silu_backward and the products around it in
-// EPMergedFc1GroupGemm.backward, veomni/distributed/moe/moe_layer.py:453-482,
-// :479): dact is the bf16 dgrad output,
-//   s = bf16(silu(g)), d_silu = bf16(dact * u), sig = sigmoid(g)
-//   dgate = d_silu * sig * (1 + g * (1 - sig)),  dup = s * dact,
-// with sig * (1 + g * (1 - sig)) evaluated as sig + silu(g) * (1 - sig) in
-// one fma (fp32 rounding differs from aten's order by a few ulp).
-__device__ __forceinline__ void swiglu_bwd8(const float* dact, const float* g, const float* u, float* dgate,
-                                            float* dup) {
-#pragma unroll
-  for (int q = 0; q < 8; q += 2) {
-    const float sig0 = sigmoid_f32(g[q]), sig1 = sigmoid_f32(g[q + 1]);
-    const float gs0 = g[q] * sig0, gs1 = g[q + 1] * sig1;
-    float s0 = gs0, s1 = gs1;
-    float d0 = dact[q] * u[q], d1 = dact[q + 1] * u[q + 1];
-    round2_bf16(s0, s1);
-    round2_bf16(d0, d1);
-    dgate[q] = d0 * __builtin_fmaf(gs0, 1.0f - sig0, sig0);
-    dgate[q + 1] = d1 * __builtin_fmaf(gs1, 1.0f - sig1, sig1);
-    dup[q] = s0 * dact[q];
-    dup[q + 1] = s1 * dact[q + 1];
-  }
-}
-
 __device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) { return make_uint2(pack2(a, b), pack2(c, d)); }
 __device__ __forceinline__ uint2 acc4(const f32x16_t& a, int i) { return pack4(a[i], a[i + 1], a[i + 2], a[i + 3]); }
 

@@ -615,7 +615,6 @@ __global__ __launch_bounds__(256) void combine_bwd_top1_kernel(const bf16_t* __r
   if (lane == 0) dw[t] = (bf16_t)f32_to_bf16(part);
 }
 
-// order[pos[i]] = i : the inverse of the stable scatter index.
 // Top-1 combine gradient in the rows' storage order: wave r handles row r of
 // Y and dY (read and written front to back) and gathers its token's dout row.
 // On the DeepSeek-V3-shape rows (65536 x 7168, a random row order) this moves
@@ -671,6 +670,7 @@ __global__ __launch_bounds__(256) void combine_bwd_top1_rows_kernel(const bf16_t
   if (lane == 0 && ok) dw[t] = (bf16_t)f32_to_bf16(part);
 }
 
+// order[pos[i]] = i : the inverse of the stable scatter index.
 __global__ void invert_kernel(const int32_t* __restrict__ pos, int64_t N, int32_t* __restrict__ order) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < N) order[pos[i]] = (int32_t)i;

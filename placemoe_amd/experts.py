@@ -15,6 +15,14 @@ branch of ``group_gemm_fused_moe_forward``
 per-copy contiguous rows, ``EPMergedFc1GroupGemm`` / ``EPGroupGemm``
 (veomni/distributed/moe/moe_layer.py:147-547), router weights applied in the
 combine (``rank_dedup_combine``, veomni/distributed/moe/hiermoe/all_to_all.py:2539-2564).
+
+``weighted_input=True`` gives the arithmetic of the reference's non-EP
+branch instead (``TritonFusedMoeExpertFunction`` /
+``MergedFc1TritonFusedMoeExpertFunction``, group_gemm.py:210-631): each row's
+SwiGLU output is multiplied by its router weight before fc2, the top-k rows
+of a token are summed unweighted (``moe_gather``), and the backward takes the
+router-weight gradient from the fc2 input side.  The two agree in exact
+arithmetic and differ in bf16 rounding.
 """
 
 from __future__ import annotations
@@ -131,7 +139,7 @@ class _ExpertLayerBase(torch.autograd.Function):
 
     @staticmethod
     def _forward(ctx, hidden, routing_weights, selected, mapping, sources, source, w_gate, w_up, copy_stride,
-                 fc2_weight, split, recorder):
+                 fc2_weight, split, recorder, weighted_input):
         T, H = hidden.shape
         C, H2, inter = fc2_weight.shape
         assert H2 == H, f"down_proj hidden size {H2} != hidden size {H}"
@@ -158,6 +166,21 @@ class _ExpertLayerBase(torch.autograd.Function):
             _PENDING_CHECKS.append(check)
         if recorder is not None:
             recorder(r.counts)
+        ctx.split = split
+        ctx.inter = inter
+        ctx.routing = r
+        ctx.weighted_input = weighted_input
+        if weighted_input:
+            # group_gemm.py:473-511: fc1_weighted_output = fc1_activation *
+            # scattered_gate_weight feeds fc2; moe_gather sums a token's rows.
+            xp, row_src, row_w = kernels.moe_scatter_src(hidden, r.pos, routing_weights)
+            gu, act = kernels.gemm_fc1_swiglu(xp, w_gate, w_up, copy_stride, r.offsets, C, inter)
+            act_w = kernels.weight_rows(act, row_w)
+            y = kernels.group_gemm_nt(act_w, fc2_weight, r.offsets)
+            out = kernels.moe_gather(y, r.pos)
+            ctx.save_for_backward(xp, gu, act, act_w, r.pos, r.offsets, routing_weights, w_gate, w_up, fc2_weight,
+                                  row_src, row_w)
+            return out
         row_src = None
         if r.pos.shape[1] == 1 and _TOP1_FUSION:
             xp, row_src, row_w = kernels.moe_scatter_src(hidden, r.pos, routing_weights)
@@ -170,14 +193,13 @@ class _ExpertLayerBase(torch.autograd.Function):
             y = kernels.group_gemm_nt(act, fc2_weight, r.offsets)
             out = kernels.combine_fwd(y, r.pos, routing_weights)
         ctx.save_for_backward(xp, gu, act, y, r.pos, r.offsets, routing_weights, w_gate, w_up, fc2_weight, row_src)
-        ctx.split = split
-        ctx.inter = inter
-        ctx.routing = r
         return out
 
     @staticmethod
     def _backward(ctx, grad_out):
         _poll_pending_checks()
+        if ctx.weighted_input:
+            return _ExpertLayerBase._backward_weighted_input(ctx, grad_out)
         xp, gu, act, y, pos, offsets, w, w_gate, w_up, fc2_weight, row_src = ctx.saved_tensors
         grad_out = grad_out.contiguous()
         need_w, need_x = ctx.needs_input_grad[1], ctx.needs_input_grad[0]
@@ -219,13 +241,51 @@ class _ExpertLayerBase(torch.autograd.Function):
                     t.record_stream(main)
         return dx, (dw if need_w else None), d_fc1, d_fc2
 
+    @staticmethod
+    def _backward_weighted_input(ctx, grad_out):
+        """group_gemm.py:533-629: grad_fc2_output = moe_scatter(grad_output);
+        its dgrad through fc2, then the router weight's backward with the
+        SwiGLU backward in one row kernel; fc1 as in the EP branch."""
+        xp, gu, act, act_w, pos, offsets, w, w_gate, w_up, fc2_weight, row_src, row_w = ctx.saved_tensors
+        grad_out = grad_out.contiguous()
+        need_w, need_x = ctx.needs_input_grad[1], ctx.needs_input_grad[0]
+        dyp = kernels.moe_scatter(grad_out, pos)
+        main = torch.cuda.current_stream(dyp.device)
+        side = _side_stream(dyp.device) if uses_backward_overlap(dyp.shape[0], dyp.shape[1], ctx.inter) else main
+        d_fc2 = d_fc1 = None
+        if ctx.fc2_needs_grad:
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                d_fc2 = kernels.group_gemm_tn(dyp, act_w, offsets)
+        d_act_w = kernels.group_gemm_nn(dyp, fc2_weight, offsets)
+        dg1, dw = kernels.swiglu_bwd_weighted(d_act_w, gu, act, row_w, row_src, pos.numel())
+        if ctx.fc1_needs_grad:
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                d_fc1 = kernels.group_gemm_tn(dg1, xp, offsets, split=ctx.inter if ctx.split else None)
+        dx = None
+        if need_x:
+            b_second = w_up if ctx.split else None
+            if pos.shape[1] == 1 and _TOP1_FUSION:
+                # top-1: row_src[r] is row r's token
+                dx = kernels.group_gemm_nn_unpermute_top1(dg1, w_gate, offsets, row_src, b_second=b_second)
+            else:
+                dxp = kernels.group_gemm_nn(dg1, w_gate, offsets, b_second=b_second)
+                dx = kernels.moe_gather(dxp, pos)
+        if side is not main:
+            main.wait_stream(side)
+            for t in (d_fc2, *(d_fc1 if isinstance(d_fc1, tuple) else (d_fc1,))):
+                if t is not None:
+                    t.record_stream(main)
+        return dx, (dw.view(w.shape) if need_w else None), d_fc1, d_fc2
+
 
 class HipMergedFc1ExpertLayer(_ExpertLayerBase):
     """Merged ``gate_up_proj`` [C, 2I, H] (``EPMergedFc1GroupGemm`` layout)."""
 
     @staticmethod
     def forward(ctx, hidden, routing_weights, selected, mapping, sources, source, fc1_1_2_weight, fc2_weight,
-                recorder=None):
+                recorder=None, weighted_input=False):
         C, two_i, H = fc1_1_2_weight.shape
         assert two_i % 2 == 0, f"Merged fc1_1_2_weight dim 1 must be even, got {two_i}"
         inter = two_i // 2
@@ -235,13 +295,13 @@ class HipMergedFc1ExpertLayer(_ExpertLayerBase):
         ctx.fc2_needs_grad = ctx.needs_input_grad[7]
         return _ExpertLayerBase._forward(
             ctx, hidden, routing_weights, selected, mapping, sources, source, fc1_1_2_weight, w_up,
-            2 * inter * H, fc2_weight, False, recorder,
+            2 * inter * H, fc2_weight, False, recorder, weighted_input,
         )
 
     @staticmethod
     def backward(ctx, grad_out):
         dx, dw, d_fc1, d_fc2 = _ExpertLayerBase._backward(ctx, grad_out)
-        return dx, dw, None, None, None, None, d_fc1, d_fc2, None
+        return dx, dw, None, None, None, None, d_fc1, d_fc2, None, None
 
 
 class HipSplitFc1ExpertLayer(_ExpertLayerBase):
@@ -249,7 +309,7 @@ class HipSplitFc1ExpertLayer(_ExpertLayerBase):
 
     @staticmethod
     def forward(ctx, hidden, routing_weights, selected, mapping, sources, source, fc1_1_weight, fc1_2_weight,
-                fc2_weight, recorder=None):
+                fc2_weight, recorder=None, weighted_input=False):
         C, inter, H = fc1_1_weight.shape
         assert fc1_2_weight.shape == fc1_1_weight.shape, "fc1_1 and fc1_2 shapes differ"
         assert fc1_1_weight.is_contiguous() and fc1_2_weight.is_contiguous() and fc2_weight.is_contiguous(), (
@@ -259,14 +319,14 @@ class HipSplitFc1ExpertLayer(_ExpertLayerBase):
         ctx.fc2_needs_grad = ctx.needs_input_grad[8]
         return _ExpertLayerBase._forward(
             ctx, hidden, routing_weights, selected, mapping, sources, source, fc1_1_weight, fc1_2_weight,
-            inter * H, fc2_weight, True, recorder,
+            inter * H, fc2_weight, True, recorder, weighted_input,
         )
 
     @staticmethod
     def backward(ctx, grad_out):
         dx, dw, d_fc1, d_fc2 = _ExpertLayerBase._backward(ctx, grad_out)
         d_gate, d_up = d_fc1 if d_fc1 is not None else (None, None)
-        return dx, dw, None, None, None, None, d_gate, d_up, d_fc2, None
+        return dx, dw, None, None, None, None, d_gate, d_up, d_fc2, None, None
 
 
 def expert_layer(
@@ -281,6 +341,7 @@ def expert_layer(
     sources: torch.Tensor | None = None,
     source: int = 0,
     recorder=None,
+    weighted_input: bool = False,
 ) -> torch.Tensor:
     """The full layer on one GPU: [T, H] -> [T, H], differentiable in hidden,
     routing weights and the expert weights.
@@ -288,17 +349,19 @@ def expert_layer(
     ``mapping`` [S, E] maps (source, logical expert) to a physical copy (slot)
     of ``fc2_weight.shape[0]`` copies; None means slot == logical expert.
     ``recorder(counts)`` receives the int32 per-copy token counts (on the device).
+    ``weighted_input``: apply the router weights to the fc2 input (the
+    reference's non-EP arithmetic) instead of in the combine (EP).
     """
     if fc1_1_2_weight is not None:
         if fc1_1_weight is not None or fc1_2_weight is not None:
             raise ValueError("Provide either split fc1 weights or merged fc1_1_2_weight, not both.")
         return HipMergedFc1ExpertLayer.apply(
             hidden, routing_weights, selected_experts, mapping, sources, source, fc1_1_2_weight, fc2_weight,
-            recorder,
+            recorder, bool(weighted_input),
         )
     if fc1_1_weight is None or fc1_2_weight is None:
         raise ValueError("Split fc1 mode requires both fc1_1_weight and fc1_2_weight.")
     return HipSplitFc1ExpertLayer.apply(
         hidden, routing_weights, selected_experts, mapping, sources, source, fc1_1_weight, fc1_2_weight, fc2_weight,
-        recorder,
+        recorder, bool(weighted_input),
     )

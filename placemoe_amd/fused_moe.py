@@ -17,6 +17,12 @@ veomni/ops/kernels/moe/__init__.py:
 ``group_gemm_fused_moe_forward``, veomni/ops/kernels/moe/group_gemm.py:634-961):
 with a registered ``LayerPlacement`` for ``layer_key`` it applies the
 source-aware ``M`` table, otherwise every logical expert is its own slot.
+
+Where the router weights enter follows the reference's two branches
+(group_gemm.py:655, :937-961): a layer with a registered placement (PlaceMoE
+runs under expert parallelism) gets the EP arithmetic, weights applied in the
+combine; a layer without one gets the non-EP arithmetic, weights applied to
+the fc2 input.  ``set_router_weight_point`` fixes either for every layer.
 """
 
 from __future__ import annotations
@@ -28,6 +34,24 @@ from .kernel_registry import KERNEL_REGISTRY, HardwareRequirement, KernelSpec
 from .placement import PLACEMENTS
 
 _fused_moe_forward = None
+
+# "auto" (by placement, as above), "combine" (EP arithmetic) or "fc2_input"
+# (non-EP arithmetic).
+_ROUTER_WEIGHT_POINTS = ("auto", "combine", "fc2_input")
+_ROUTER_WEIGHT_POINT = "auto"
+
+
+def set_router_weight_point(point: str) -> str:
+    """Where the hip backend applies the router weights: ``"combine"`` (the
+    EP branch's ``rank_dedup_combine``), ``"fc2_input"`` (the non-EP branch's
+    ``fc1_activation * scattered_gate_weight``) or ``"auto"`` (the default:
+    ``"combine"`` for layers with a registered placement, else
+    ``"fc2_input"``).  Returns the previous setting."""
+    global _ROUTER_WEIGHT_POINT
+    if point not in _ROUTER_WEIGHT_POINTS:
+        raise ValueError(f"router weight point must be one of {_ROUTER_WEIGHT_POINTS}, got {point!r}")
+    prev, _ROUTER_WEIGHT_POINT = _ROUTER_WEIGHT_POINT, point
+    return prev
 
 
 def fused_moe_forward(
@@ -102,9 +126,13 @@ def hip_fused_moe_forward(
         raise ValueError(
             f"{int(fc2_weight.shape[0])} expert weights cannot serve {num_experts} experts without a placement"
         )
+    point = _ROUTER_WEIGHT_POINT
+    if point == "auto":
+        point = "combine" if placement is not None else "fc2_input"
     out = expert_layer(
         hidden, w, sel, fc2_weight, fc1_1_2_weight=fc1_1_2_weight, fc1_1_weight=fc1_1_weight,
         fc1_2_weight=fc1_2_weight, mapping=mapping, sources=sources, source=source, recorder=recorder,
+        weighted_input=point == "fc2_input",
     )
     return out.reshape(shape)
 

@@ -389,6 +389,39 @@ def gemm_fc2_dgrad_swiglu(dy: torch.Tensor, w_down: torch.Tensor, gu: torch.Tens
     return dg1
 
 
+def weight_rows(act: torch.Tensor, row_w: torch.Tensor) -> torch.Tensor:
+    """out[r] = bf16(act[r] * row_w[r]) -> [R, N]: the router weight applied
+    to the fc2 input (the reference's non-EP path)."""
+    dev = _check_dev(act, row_w)
+    _bf16("act", act)
+    _bf16("row weights", row_w)
+    R, N = act.shape
+    assert row_w.numel() == R and row_w.is_contiguous(), "one router weight per row"
+    out = torch.empty_like(act)
+    _capi.call("pmx_weight_rows", _ptr(act), _ptr(row_w), R, N, _ptr(out), _stream(dev))
+    return out
+
+
+def swiglu_bwd_weighted(d_act_w: torch.Tensor, gu: torch.Tensor, act: torch.Tensor, row_w: torch.Tensor,
+                        row_src: torch.Tensor, num_assign: int):
+    """Backward of ``weight_rows`` and the SwiGLU forward, per row:
+    dG1 [R, 2I] from dact = bf16(d_act_w * row_w), and the router-weight
+    gradient dw[row_src[r]] = bf16(sum_j bf16(act[r,j] * d_act_w[r,j]))
+    -> (dG1, dw [num_assign] bf16; entries no row names are not written)."""
+    dev = _check_dev(d_act_w, gu, act, row_w, row_src)
+    for name, t in (("d_act_w", d_act_w), ("gu", gu), ("act", act), ("row weights", row_w)):
+        _bf16(name, t)
+    R, I = act.shape
+    assert d_act_w.shape == (R, I) and gu.shape == (R, 2 * I), "d_act_w [R, I], gu [R, 2I]"
+    assert row_w.numel() == R and row_w.is_contiguous()
+    assert row_src.dtype == torch.int32 and row_src.is_contiguous() and row_src.numel() == R
+    dg1 = torch.empty((R, 2 * I), dtype=act.dtype, device=dev)
+    dw = torch.empty(num_assign, dtype=row_w.dtype, device=dev)
+    _capi.call("pmx_swiglu_bwd_weighted", _ptr(d_act_w), _ptr(gu), _ptr(act), _ptr(row_w), _ptr(row_src), R, I,
+               num_assign, _ptr(dg1), _ptr(dw), _stream(dev))
+    return dg1, dw
+
+
 def group_gemm_tn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, split: int | None = None):
     """C[g] = a[rows g]^T @ b[rows g] -> [G, M, N] (zeros for empty groups).
 

@@ -73,6 +73,17 @@ def test_argument_errors_are_codes_not_crashes():
     assert lib.pmx_combine_bwd_top1_rows(dummy, dummy, dummy, dummy, -1, 8, dummy, dummy, None) == _capi.PMX_ERR_ARG
     assert lib.pmx_combine_bwd_top1_rows(dummy, dummy, dummy, dummy, 4, 12, dummy, dummy, None) == _capi.PMX_ERR_SHAPE
     assert lib.pmx_combine_bwd_top1_rows(dummy, dummy, dummy, dummy, 0, 8, dummy, dummy, None) == _capi.PMX_OK
+    assert lib.pmx_weight_rows(None, None, 4, 8, None, None) == _capi.PMX_ERR_ARG
+    assert lib.pmx_weight_rows(dummy, dummy, -1, 8, dummy, None) == _capi.PMX_ERR_ARG
+    assert lib.pmx_weight_rows(dummy, dummy, 0, 8, dummy, None) == _capi.PMX_OK
+    assert lib.pmx_weight_rows(dummy, dummy, 1 << 62, 8, dummy, None) == _capi.PMX_ERR_SHAPE
+    swb = lib.pmx_swiglu_bwd_weighted
+    assert swb(dummy, dummy, dummy, dummy, dummy, 4, 8, 4, dummy, None, None) == _capi.PMX_ERR_ARG  # dw without row_src
+    assert swb(dummy, dummy, dummy, dummy, None, 4, 8, 4, dummy, dummy, None) == _capi.PMX_ERR_ARG
+    assert swb(None, None, None, None, None, 4, 8, 0, None, None, None) == _capi.PMX_ERR_ARG
+    assert swb(dummy, dummy, dummy, dummy, dummy, 4, -8, 4, dummy, dummy, None) == _capi.PMX_ERR_ARG
+    assert swb(dummy, dummy, dummy, dummy, dummy, 0, 8, 0, dummy, dummy, None) == _capi.PMX_OK
+    assert swb(dummy, dummy, dummy, dummy, dummy, 1 << 40, 8, 4, dummy, dummy, None) == _capi.PMX_ERR_SHAPE
     with pytest.raises(ValueError):
         _capi.call("pmx_group_gemm_nt", None, None, None, 4, 8, 12, 8, None, None)
 

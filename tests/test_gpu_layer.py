@@ -130,8 +130,8 @@ def test_fused_moe_forward_public_op(cuda):
         hidden_states=wl.hidden.to(cuda), fc1_1_weight=None, fc1_2_weight=None, fc2_weight=wl.fc2.to(cuda),
         fc1_1_2_weight=wl.fc1.to(cuda),
     )
-    phys = wl.selected.numpy()  # no placement registered: slot == expert id
-    fwd = O.moe_layer_forward(wl.hidden, wl.routing_weights, phys, wl.fc1, wl.fc2)
+    phys = wl.selected.numpy()  # no placement registered: slot == expert id, the non-EP arithmetic
+    fwd = O.moe_layer_forward_weighted_input(wl.hidden, wl.routing_weights, phys, wl.fc1, wl.fc2)
     assert_bf16_close(out, fwd["out"], name="fused_moe_forward")
 
 
@@ -225,10 +225,11 @@ def test_layer_with_no_tokens(cuda):
     assert torch.count_nonzero(fc1.grad).item() == 0 and torch.count_nonzero(fc2.grad).item() == 0
 
 
-@pytest.mark.parametrize("name,tokens,slots", [("qwen3", 512, None), ("dsv3", 1024, 4)])
-def test_backward_on_one_or_two_streams_is_bitwise_identical(cuda, name, tokens, slots):
+@pytest.mark.parametrize("name,tokens,slots,weighted_input", [
+    ("qwen3", 512, None, False), ("dsv3", 1024, 4, False), ("qwen3", 512, None, True), ("dsv3", 1024, 4, True)])
+def test_backward_on_one_or_two_streams_is_bitwise_identical(cuda, name, tokens, slots, weighted_input):
     wl = make_workload(name, tokens=tokens, num_slots=slots)
-    print(f"backward streams {name}: T={wl.T} K={wl.K} C={wl.C}", flush=True)
+    print(f"backward streams {name}: T={wl.T} K={wl.K} C={wl.C} weighted_input={weighted_input}", flush=True)
     dout = torch.randn((wl.T, wl.H), generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(cuda)
     src = None if wl.sources is None else wl.sources.to(cuda)
     results = []
@@ -241,7 +242,7 @@ def test_backward_on_one_or_two_streams_is_bitwise_identical(cuda, name, tokens,
             fc1 = wl.fc1.to(cuda).requires_grad_(True)
             fc2 = wl.fc2.to(cuda).requires_grad_(True)
             out = experts.expert_layer(x, w, wl.selected.to(cuda), fc2, fc1_1_2_weight=fc1,
-                                       mapping=wl.mapping.to(cuda), sources=src)
+                                       mapping=wl.mapping.to(cuda), sources=src, weighted_input=weighted_input)
             out.backward(dout)
             torch.cuda.synchronize()
             results.append([t.clone() for t in (x.grad, w.grad, fc1.grad, fc2.grad)])

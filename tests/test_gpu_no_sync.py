@@ -3,7 +3,8 @@ its fused forward under (tests/models/test_model_forward_no_implicit_sync.py:
 129-133, 665-677, with torch's sync debug mode).
 
 Two checks at the Qwen3-30B-A3B layer shape (512 tokens, 128 experts on 160
-copies, source-aware M, top-8), forward and backward through the public op:
+copies, source-aware M, top-8; and without a placement, 128 experts, where the
+op takes the non-EP arithmetic), forward and backward through the public op:
   - torch's sync debug mode set to "error" raises on any synchronising torch
     call inside the op;
   - behind a bounded spin kernel queued first on the stream, the host
@@ -27,22 +28,28 @@ KEY = "layers.0.mlp.experts"
 
 
 class _Case:
-    def __init__(self, cuda):
+    def __init__(self, cuda, placed):
         placemoe_amd.apply_veomni_fused_moe_patch("hip")
         wl = make_workload("qwen3", tokens=512)
-        plan = LayerPlan(slot_to_logical=wl.slot_to_logical, source_logical_to_physical=wl.mapping.numpy(),
-                         owner_slots=wl.owner_slots())
-        self.placement = LayerPlacement.from_plan(KEY, plan, wl.num_experts)
-        self.placement.token_sources = wl.sources.to(cuda)
+        self.placement = None
         self.E = wl.num_experts
         self.x = wl.hidden.to(cuda)
         self.w = wl.routing_weights.to(cuda)
         self.sel = wl.selected.to(cuda)
-        self.fc1 = wl.fc1.to(cuda)
-        self.fc2 = wl.fc2.to(cuda)
+        if placed:
+            plan = LayerPlan(slot_to_logical=wl.slot_to_logical, source_logical_to_physical=wl.mapping.numpy(),
+                             owner_slots=wl.owner_slots())
+            self.placement = LayerPlacement.from_plan(KEY, plan, wl.num_experts)
+            self.placement.token_sources = wl.sources.to(cuda)
+            self.fc1 = wl.fc1.to(cuda)
+            self.fc2 = wl.fc2.to(cuda)
+        else:
+            # one copy per logical expert: slot == expert id
+            first = [list(wl.slot_to_logical).index(e) for e in range(wl.num_experts)]
+            self.fc1 = wl.fc1[first].contiguous().to(cuda)
+            self.fc2 = wl.fc2[first].contiguous().to(cuda)
         g = torch.Generator(device=cuda).manual_seed(5)
         self.dout = torch.randn(self.x.shape, generator=g, device=cuda).to(torch.bfloat16)
-        PLACEMENTS.register(self.placement, self.fc1, self.fc2)
 
     def step(self):
         """One forward + backward; returns the four gradients."""
@@ -50,7 +57,8 @@ class _Case:
         w = self.w.detach().requires_grad_(True)
         fc1 = self.fc1.detach().requires_grad_(True)
         fc2 = self.fc2.detach().requires_grad_(True)
-        PLACEMENTS.register(self.placement, fc1, fc2)
+        if self.placement is not None:
+            PLACEMENTS.register(self.placement, fc1, fc2)
         out = placemoe_amd.fused_moe_forward(
             num_experts=self.E, routing_weights=w, selected_experts=self.sel, hidden_states=x,
             fc1_1_weight=None, fc1_2_weight=None, fc2_weight=fc2, fc1_1_2_weight=fc1)
@@ -58,9 +66,9 @@ class _Case:
         return out, x.grad, w.grad, fc1.grad, fc2.grad
 
 
-@pytest.fixture
-def case(cuda):
-    c = _Case(cuda)
+@pytest.fixture(params=[True, False], ids=["placed_ep", "unplaced_non_ep"])
+def case(cuda, request):
+    c = _Case(cuda, request.param)
     try:
         yield c
     finally:

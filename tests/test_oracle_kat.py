@@ -205,6 +205,77 @@ def test_planted_transposed_operand_is_caught():
     assert err_good < 2e-2 < err_bad
 
 
+def _layer_case(seed, T=24, K=2, H=32, I=16, C=5, w=None):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((T, H), generator=g).to(BF)
+    if w is None:
+        w = torch.rand((T, K), generator=g).to(BF)
+    phys = np.random.default_rng(seed).integers(0, C, size=(T, K))
+    phys[0, :] = C - 1  # a token routed twice to the same copy
+    w1 = (torch.randn((C, 2 * I, H), generator=g) * 0.2).to(BF)
+    w2 = (torch.randn((C, H, I), generator=g) * 0.2).to(BF)
+    dout = torch.randn((T, H), generator=g).to(BF)
+    return x, w, phys, w1, w2, dout
+
+
+def test_weighted_input_layer_against_float64_autograd():
+    """The non-EP branch (router weight on the fc2 input) computes the same
+    function as the eager loop, which applies it after fc2: they agree in
+    exact arithmetic."""
+    x, w, phys, w1, w2, dout = _layer_case(12)
+    fwd = O.moe_layer_forward_weighted_input(x, w, phys, w1, w2)
+    bwd = O.moe_layer_backward_weighted_input(dout, fwd, w, w1, w2)
+    xd, wd = x.double().requires_grad_(True), w.double().requires_grad_(True)
+    w1d, w2d = w1.double().requires_grad_(True), w2.double().requires_grad_(True)
+    ref = _eager_moe_f64(xd, wd, phys, w1d, w2d)
+    ref.backward(dout.double())
+    for name, a, b, tol in (("out", fwd["out"], ref.detach(), 2e-2), ("dx", bwd["dx"], xd.grad, 3e-2),
+                            ("dw", bwd["dw"], wd.grad, 3e-2), ("dw1", bwd["dw1"], w1d.grad, 3e-2),
+                            ("dw2", bwd["dw2"], w2d.grad, 3e-2)):
+        err = (a.double() - b).abs().max().item() / b.abs().max().item()
+        assert err < tol, f"{name}: {err}"
+
+
+def test_weighted_input_equals_ep_for_power_of_two_weights():
+    """With router weights 2^-j every product with a weight is exact, so the
+    two branches round at the same values: output, dx, dw1 and dw2 agree bit
+    for bit; dw is summed over different products (dout * y against
+    act * d_act_w) and agrees within the bf16 bar."""
+    T, K = 24, 2
+    j = torch.as_tensor(np.random.default_rng(7).integers(0, 6, size=(T, K)))
+    w = torch.pow(2.0, -j.double()).to(BF)
+    x, w, phys, w1, w2, dout = _layer_case(13, T=T, K=K, w=w)
+    ep = O.moe_layer_forward(x, w, phys, w1, w2)
+    ni = O.moe_layer_forward_weighted_input(x, w, phys, w1, w2)
+    assert torch.equal(ep["out"], ni["out"])
+    bep = O.moe_layer_backward(dout, ep, w, w1, w2)
+    bni = O.moe_layer_backward_weighted_input(dout, ni, w, w1, w2)
+    for k in ("dx", "dw1", "dw2", "dg1"):
+        assert torch.equal(bep[k], bni[k]), k
+    err = (bni["dw"].float() - bep["dw"].float()).abs().max() / bep["dw"].float().abs().max()
+    assert err < 1e-2
+    # and with general weights the two branches do differ (in bf16 rounding)
+    x, w, phys, w1, w2, dout = _layer_case(13, T=T, K=K)
+    assert not torch.equal(O.moe_layer_forward(x, w, phys, w1, w2)["out"],
+                           O.moe_layer_forward_weighted_input(x, w, phys, w1, w2)["out"])
+
+
+def test_weighted_input_planted_missing_weight_is_caught():
+    """A backward that forgets the router weight in dact (planted here, in a
+    copy of the oracle's steps) must fail the float64 model check."""
+    x, w, phys, w1, w2, dout = _layer_case(14)
+    fwd = O.moe_layer_forward_weighted_input(x, w, phys, w1, w2)
+    pos, off = fwd["pos"], fwd["offsets"]
+    d_act_w = O.grouped_gemm_nn(O.permute(dout, pos), w2, off)
+    dg1_bad, _ = O.swiglu_backward_weighted(d_act_w, fwd["gu"], fwd["act"], torch.ones_like(fwd["row_w"]))
+    dx_bad = O.unpermute_grad(O.grouped_gemm_nn(dg1_bad, w1, off), pos)
+    dx_good = O.moe_layer_backward_weighted_input(dout, fwd, w, w1, w2)["dx"]
+    xd = x.double().requires_grad_(True)
+    _eager_moe_f64(xd, w.double(), phys, w1.double(), w2.double()).backward(dout.double())
+    err = lambda a: ((a.double() - xd.grad).abs().max() / xd.grad.abs().max()).item()  # noqa: E731
+    assert err(dx_good) < 3e-2 < err(dx_bad)
+
+
 # --------------------------------------------------------------------------- combine
 
 
