@@ -11,7 +11,8 @@
  *    allocated by the caller.  The library allocates nothing, never
  *    synchronises the host, and enqueues work only on the given stream.
  *  - bf16 tensors are passed as `const void*` holding bf16 bit patterns,
- *    row-major and contiguous.  Index tensors are int32 unless stated.
+ *    row-major and contiguous (fp16 tensors go to the *_f16 entry points,
+ *    see "fp16 tensors" at the end).  Index tensors are int32 unless stated.
  *  - Positions, row offsets and the row kernels' token rows are 32-bit:
  *    assignments T*K, GEMM row counts and segment-sum rows above 2^31-1
  *    return PMX_ERR_SHAPE before anything is launched.
@@ -308,6 +309,7 @@ int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const int32_t* co
 /* Gradient element types of the exchange entry points. */
 #define PMX_DTYPE_BF16 0
 #define PMX_DTYPE_F32 1
+#define PMX_DTYPE_F16 2
 
 /* An exchange item is one logical expert x one parameter.  grads: [C, P]
  * copy gradients of this rank (`dtype`), item i's local copies are
@@ -413,6 +415,64 @@ int pmx_ep_combine_aggregate(const void* Y, const int32_t* pos, const void* w, c
                              int32_t* run_offsets, int32_t* rank_runs, int32_t* num_runs,
                              int32_t* status, void* workspace, size_t workspace_bytes,
                              pmx_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* fp16 tensors                                                              */
+/* ------------------------------------------------------------------------ */
+/* The reference's fused MoE op takes bf16 or fp16 hidden states and router
+ * weights (veomni/ops/kernels/moe/__init__.py:44-49) and computes in the
+ * input dtype: fp32 accumulation, every rounding point in that dtype.  Each
+ * entry point below is its namesake above for fp16 tensors: same arguments,
+ * same checks and error codes, and every "bf16(...)" of its description is
+ * round-to-nearest-even to fp16 (overflow gives inf).  The routing entry
+ * points and the row copies (pmx_moe_scatter, pmx_moe_scatter_src,
+ * pmx_ep_dispatch_payload) move 16-bit patterns and serve both types;
+ * pmx_replica_exchange_pack/unpack take PMX_DTYPE_F16. */
+
+int pmx_moe_gather_f16(const void* Y, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* out,
+                       pmx_stream_t stream);
+int pmx_combine_fwd_f16(const void* Y, const int32_t* pos, const void* w, int64_t T, int32_t K, int64_t H,
+                        void* out, pmx_stream_t stream);
+int pmx_combine_bwd_f16(const void* dout, const void* Y, const int32_t* pos, const void* w, int64_t T,
+                        int32_t K, int64_t H, void* dY, void* dw, pmx_stream_t stream);
+int pmx_combine_bwd_top1_rows_f16(const void* dout, const void* Y, const int32_t* row_token, const void* w,
+                                  int64_t T, int64_t H, void* dY, void* dw, pmx_stream_t stream);
+int pmx_segment_sum_f16(const void* source, const int64_t* index, int64_t N, int64_t H, int64_t num_rows,
+                        void* out, void* workspace, size_t workspace_bytes, pmx_stream_t stream);
+int pmx_gemm_fc1_swiglu_fwd_f16(const void* X, const void* w_gate, const void* w_up, int64_t w_copy_stride,
+                                const int32_t* offsets, int32_t G, int64_t A, int64_t H, int64_t I, void* gu,
+                                void* act, pmx_stream_t stream);
+int pmx_group_gemm_nt_f16(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M,
+                          int64_t N, int64_t K, void* C, pmx_stream_t stream);
+int pmx_group_gemm_nt_combine_top1_f16(const void* A, const void* B, const int32_t* offsets, int32_t G,
+                                       int64_t M, int64_t N, int64_t K, void* C, const int32_t* row_token,
+                                       const void* row_weight, void* out, pmx_stream_t stream);
+int pmx_group_gemm_nn_f16(const void* A, const void* B0, const void* B1, int64_t b_copy_stride,
+                          int64_t b_split, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
+                          int64_t K, void* C, pmx_stream_t stream);
+int pmx_group_gemm_nn_unpermute_top1_f16(const void* A, const void* B0, const void* B1,
+                                         int64_t b_copy_stride, int64_t b_split, const int32_t* offsets,
+                                         int32_t G, int64_t M, int64_t N, int64_t K,
+                                         const int32_t* row_token, void* C, pmx_stream_t stream);
+int pmx_gemm_fc2_dgrad_swiglu_bwd_f16(const void* dY, const void* w_down, const void* gu,
+                                      const int32_t* offsets, int32_t G, int64_t A, int64_t H, int64_t I,
+                                      void* dG1, pmx_stream_t stream);
+int pmx_group_gemm_tn_f16(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t K,
+                          int64_t M, int64_t N, void* C0, void* C1, int64_t c_copy_stride, int64_t c_split,
+                          pmx_stream_t stream);
+int pmx_weight_rows_f16(const void* act, const void* row_w, int64_t R, int64_t N, void* out,
+                        pmx_stream_t stream);
+int pmx_swiglu_bwd_weighted_f16(const void* d_act_w, const void* gu, const void* act, const void* row_w,
+                                const int32_t* row_src, int64_t R, int64_t I, int64_t A, void* dG1, void* dw,
+                                pmx_stream_t stream);
+int pmx_replica_fold_f16(void* grads, const int32_t* copy_offsets, const int32_t* copy_slots,
+                         const int64_t* slot_tokens, int32_t E, int32_t C, int64_t P, float* out,
+                         int32_t writeback, int32_t* status, pmx_stream_t stream);
+int pmx_ep_combine_aggregate_f16(const void* Y, const int32_t* pos, const void* w, const int32_t* src_rank,
+                                 const int32_t* src_token, int64_t N, int64_t H, int32_t R, void* out,
+                                 int32_t* run_offsets, int32_t* rank_runs, int32_t* num_runs,
+                                 int32_t* status, void* workspace, size_t workspace_bytes,
+                                 pmx_stream_t stream);
 
 #ifdef __cplusplus
 }

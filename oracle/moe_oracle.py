@@ -8,7 +8,8 @@ library and nothing else: only ``tests/``, ``__graft_entry__.smoke()`` and the
 (``placemoe_amd``) never imports it and has no CPU fallback.
 
 Integer work is numpy; floating-point work is torch on the CPU in float32
-with bf16 rounding at the points where the reference stores bf16 tensors.
+with bf16 rounding at the points where the reference stores bf16 tensors
+(fp16 rounding at the same points for fp16 inputs).
 
 Reference citations are paths under the reference repository
 (pia7a/PlaceMoE), ``file:line``.
@@ -206,20 +207,24 @@ def silu_f32(x: torch.Tensor) -> torch.Tensor:
 
 def swiglu_forward(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """act = bf16(bf16(silu(gate)) * up) - the two bf16 ops of
-    veomni/distributed/moe/moe_layer.py:394-397 (``aten.silu`` then ``*``)."""
-    s = silu_f32(gate.float()).to(BF16)
-    return (s.float() * up.float()).to(BF16)
+    veomni/distributed/moe/moe_layer.py:394-397 (``aten.silu`` then ``*``).
+    Every rounding point here and below is the inputs' dtype (bf16, or fp16
+    for fp16 tensors, as the reference's ops compute in the input dtype)."""
+    dt = gate.dtype
+    s = silu_f32(gate.float()).to(dt)
+    return (s.float() * up.float()).to(dt)
 
 
 def swiglu_backward(dact: torch.Tensor, gate: torch.Tensor, up: torch.Tensor):
     """Returns (d_gate, d_up) with the reference's bf16 rounding points
     (veomni/distributed/moe/moe_layer.py:465-482)."""
+    dt = dact.dtype
     g = gate.float()
-    s = silu_f32(g).to(BF16).float()
-    d_up = (s * dact.float()).to(BF16)
-    d_silu = (dact.float() * up.float()).to(BF16).float()
+    s = silu_f32(g).to(dt).float()
+    d_up = (s * dact.float()).to(dt)
+    d_silu = (dact.float() * up.float()).to(dt).float()
     sig = torch.sigmoid(g)
-    d_gate = (d_silu * (sig * (1.0 + g * (1.0 - sig)))).to(BF16)
+    d_gate = (d_silu * (sig * (1.0 + g * (1.0 - sig)))).to(dt)
     return d_gate, d_up
 
 
@@ -271,7 +276,7 @@ def combine_forward(y: torch.Tensor, pos, w: torch.Tensor) -> torch.Tensor:
     acc = torch.zeros((T, y.shape[1]), dtype=torch.float32)
     for k in range(K):
         rows = y[pos_t[:, k]].float()
-        acc += (rows * w[:, k : k + 1].float()).to(BF16).float()
+        acc += (rows * w[:, k : k + 1].float()).to(y.dtype).float()
     return acc.to(y.dtype)
 
 
@@ -290,7 +295,7 @@ def combine_backward(dout: torch.Tensor, y: torch.Tensor, pos, w: torch.Tensor):
     for k in range(K):
         rows = y[pos_t[:, k]].float()
         dy[pos_t[:, k]] = (d * w[:, k : k + 1].float()).to(y.dtype)
-        dw[:, k] = (d * rows).to(BF16).float().sum(dim=1).to(w.dtype)
+        dw[:, k] = (d * rows).to(y.dtype).float().sum(dim=1).to(w.dtype)
     return dy, dw
 
 
@@ -400,8 +405,9 @@ def swiglu_backward_weighted(d_act_w: torch.Tensor, gu: torch.Tensor, act: torch
     bf16(sum_j fp32(bf16(act * d_act_w))) (``torch.sum`` of a bf16 product),
     then silu_backward and the up-projection product as in the EP branch."""
     I = act.shape[1]
-    dact = (d_act_w.float() * row_w.float()[:, None]).to(BF16)
-    dw_row = (act.float() * d_act_w.float()).to(BF16).float().sum(dim=1).to(row_w.dtype)
+    dt = d_act_w.dtype
+    dact = (d_act_w.float() * row_w.float()[:, None]).to(dt)
+    dw_row = (act.float() * d_act_w.float()).to(dt).float().sum(dim=1).to(row_w.dtype)
     d_gate, d_up = swiglu_backward(dact, gu[:, :I], gu[:, I:])
     return torch.cat([d_gate, d_up], dim=1), dw_row
 

@@ -134,6 +134,16 @@ SIGNATURES = {
     ),
 }
 
+# fp16 twins of the float-path entry points: the same arguments as their
+# bf16 namesakes (include/placemoe_amd.h, "fp16 tensors").
+F16_TWINS = (
+    "pmx_moe_gather", "pmx_combine_fwd", "pmx_combine_bwd", "pmx_combine_bwd_top1_rows", "pmx_segment_sum",
+    "pmx_gemm_fc1_swiglu_fwd", "pmx_group_gemm_nt", "pmx_group_gemm_nt_combine_top1", "pmx_group_gemm_nn",
+    "pmx_group_gemm_nn_unpermute_top1", "pmx_gemm_fc2_dgrad_swiglu_bwd", "pmx_group_gemm_tn", "pmx_weight_rows",
+    "pmx_swiglu_bwd_weighted", "pmx_replica_fold", "pmx_ep_combine_aggregate",
+)
+SIGNATURES.update({name + "_f16": SIGNATURES[name] for name in F16_TWINS})
+
 _LIB = None
 
 

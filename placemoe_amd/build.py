@@ -13,6 +13,9 @@ file with the compiler's per-kernel resource report and fails if any of its
 kernels uses scratch memory or spills vector registers
 (``resource_usage.json`` beside the library keeps the report).
 
+The grouped GEMM source is compiled twice into the library: once for bf16
+and once with ``-DPMX_ELT_F16`` for the fp16 entry points (``EXTRA_OBJECTS``).
+
 Test variants: ``_lib/variants/libplacemoe_amd_<name>.so`` is the same library
 with extra defines for one source (``VARIANTS``), e.g. a two-entry LDS tile
 table so that the GEMM's table-overflow path runs at small shapes.
@@ -56,6 +59,11 @@ HIP_FLAGS = [
 # docstring), and the kernel-name pattern the check applies to.
 RESOURCE_CHECKED = {"grouped_gemm.hip": re.compile(r"grouped_gemm")}
 RESOURCE_FLAG = "-Rpass-analysis=kernel-resource-usage"
+
+# name -> (source, extra flags): further objects of the library, built from a
+# source a second time with other defines.
+#   grouped_gemm.f16: the grouped GEMM for fp16 tensors (entry points *_f16).
+EXTRA_OBJECTS = {"grouped_gemm.f16": ("grouped_gemm.hip", ["-DPMX_ELT_F16"])}
 
 # name -> (source, extra flags): library variants for tests and comparisons.
 #   tiletab2: a two-entry LDS tile table (the on-the-spot tile decode runs at small shapes);
@@ -145,12 +153,14 @@ def build(verbose: bool = False) -> Path:
     obj_dir.mkdir(parents=True, exist_ok=True)
     VARIANT_DIR.mkdir(parents=True, exist_ok=True)
     jobs = [(s, obj_dir / (s.stem + ".o"), None) for s in sources]
+    for name, (src, extra) in sorted(EXTRA_OBJECTS.items()):
+        jobs.append((CSRC / src, obj_dir / f"{name}.o", extra))
     for name, (src, extra) in sorted(VARIANTS.items()):
         jobs.append((CSRC / src, obj_dir / f"{Path(src).stem}.{name}.o", extra))
     workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=workers) as pool:
         reports = list(pool.map(lambda job: _compile(*job), jobs))
-    objs = [o for _, o, _ in jobs[:len(sources)]]
+    objs = [o for _, o, _ in jobs[:len(sources) + len(EXTRA_OBJECTS)]]
     out = library_path()
     _link(objs, out)
     for name, (src, _) in sorted(VARIANTS.items()):

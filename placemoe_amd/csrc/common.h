@@ -52,6 +52,74 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
 }
 
+// 16-bit element types of the float path (bf16 and fp16).  Row copies and
+// the GEMMs' operand paths move 16-bit patterns without reading them; an
+// element type fixes only the conversions to and from fp32 (round to nearest
+// even, as torch's .to(dtype)) and, in the GEMM, the MFMA that multiplies
+// it.  to_f32 reads the low 16 bits of its argument.
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+struct EltBF16 {
+  static constexpr int kCode = 0;
+  __device__ static __forceinline__ float to_f32(uint32_t b) { return bf16_to_f32(b & 0xffffu); }
+  __device__ static __forceinline__ uint32_t pack2(float a, float b) { return ::pack2(a, b); }
+  __device__ static __forceinline__ uint32_t from_f32(float f) { return f32_to_bf16(f); }
+  __device__ static __forceinline__ float round(float f) { return round_bf16(f); }
+  __device__ static __forceinline__ void round2(float& a, float& b) { round2_bf16(a, b); }
+  __device__ static __forceinline__ void unpack2(uint32_t w, float& a, float& b) {
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  }
+};
+// fp16: gfx950 converts a pair in one v_cvt_pk_f16_f32 (round to nearest
+// even, overflow to inf) and widens with v_cvt_f32_f16 (exact).
+struct EltF16 {
+  static constexpr int kCode = 2;
+  __device__ static __forceinline__ float to_f32(uint32_t b) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xffffu));
+  }
+  __device__ static __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+  }
+  __device__ static __forceinline__ uint32_t from_f32(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+  __device__ static __forceinline__ float round(float f) { return (float)(_Float16)f; }
+  __device__ static __forceinline__ void round2(float& a, float& b) {
+    const f16x2_t h = __builtin_bit_cast(f16x2_t, pack2(a, b));
+    a = (float)h[0];
+    b = (float)h[1];
+  }
+  __device__ static __forceinline__ void unpack2(uint32_t w, float& a, float& b) {
+    const f16x2_t h = __builtin_bit_cast(f16x2_t, w);
+    a = (float)h[0];
+    b = (float)h[1];
+  }
+};
+
+// unpack8 / pack8 of either element type (element 2j in the low half of word j).
+template <class E>
+__device__ __forceinline__ void unpack8e(const uint4 v, float* f) {
+  E::unpack2(v.x, f[0], f[1]);
+  E::unpack2(v.y, f[2], f[3]);
+  E::unpack2(v.z, f[4], f[5]);
+  E::unpack2(v.w, f[6], f[7]);
+}
+template <class E>
+__device__ __forceinline__ uint4 pack8e(const float* f) {
+  return make_uint4(E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]), E::pack2(f[6], f[7]));
+}
+
+// Dispatch on the element code a C-ABI entry point passes (0 bf16, 2 fp16):
+// LAUNCH(E) with E the element type.
+#define PMX_DISPATCH_ELT(code, LAUNCH) \
+  do {                                 \
+    if ((code) == EltF16::kCode) {     \
+      LAUNCH(EltF16);                  \
+    } else {                           \
+      LAUNCH(EltBF16);                 \
+    }                                  \
+  } while (0)
+
 // 16-byte streaming (non-temporal) global load and store, for row data that
 // a kernel touches exactly once.  Measured on the row-movement kernels inside
 // the layer: streaming loads are 5-20% faster than plain loads; streaming
@@ -86,7 +154,9 @@ __device__ __forceinline__ float silu_f32(float x) { return x * sigmoid_f32(x); 
 //   s = bf16(silu(g)), d_silu = bf16(dact * u), sig = sigmoid(g)
 //   dgate = d_silu * sig * (1 + g * (1 - sig)),  dup = s * dact,
 // with sig * (1 + g * (1 - sig)) evaluated as sig + silu(g) * (1 - sig) in
-// one fma (fp32 rounding differs from aten's order by a few ulp).
+// one fma (fp32 rounding differs from aten's order by a few ulp).  E: the
+// element type whose rounding the bf16 points above take (fp16 for fp16).
+template <class E = EltBF16>
 __device__ __forceinline__ void swiglu_bwd8(const float* dact, const float* g, const float* u, float* dgate,
                                             float* dup) {
 #pragma unroll
@@ -95,8 +165,8 @@ __device__ __forceinline__ void swiglu_bwd8(const float* dact, const float* g, c
     const float gs0 = g[q] * sig0, gs1 = g[q + 1] * sig1;
     float s0 = gs0, s1 = gs1;
     float d0 = dact[q] * u[q], d1 = dact[q + 1] * u[q + 1];
-    round2_bf16(s0, s1);
-    round2_bf16(d0, d1);
+    E::round2(s0, s1);
+    E::round2(d0, d1);
     dgate[q] = d0 * __builtin_fmaf(gs0, 1.0f - sig0, sig0);
     dgate[q + 1] = d1 * __builtin_fmaf(gs1, 1.0f - sig1, sig1);
     dup[q] = s0 * dact[q];

@@ -1,4 +1,4 @@
-// Replica-gradient fold on gfx950: fp32 sum of the bf16 gradients of every
+// Replica-gradient fold on gfx950: fp32 sum of the bf16 (or fp16) gradients of every
 // physical copy of a logical expert, optionally written back to the copies.
 // A bandwidth kernel: each thread owns 8 consecutive elements of one expert
 // and streams them from every copy with 16-byte loads.
@@ -7,7 +7,7 @@
 
 namespace {
 
-template <bool VEC>
+template <class E, bool VEC>
 __global__ __launch_bounds__(256) void replica_fold_kernel(bf16_t* __restrict__ grads,
                                                            const int32_t* __restrict__ copy_offsets,
                                                            const int32_t* __restrict__ copy_slots,
@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void replica_fold_kernel(bf16_t* __restrict__ 
       }
       if (slot_tokens != nullptr && slot_tokens[c] <= 0) continue;
       float f[8];
-      unpack8(ld_stream(grads + c * P + i), f);
+      unpack8e<E>(ld_stream(grads + c * P + i), f);
 #pragma unroll
       for (int q = 0; q < 8; ++q) acc[q] += f[q];
     }
@@ -39,7 +39,7 @@ __global__ __launch_bounds__(256) void replica_fold_kernel(bf16_t* __restrict__ 
     o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
     o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
     if (writeback) {
-      const uint4 v = pack8(acc);
+      const uint4 v = pack8e<E>(acc);
       for (int32_t j = b; j < end; ++j) {
         const int64_t c = copy_slots[j];
         if (c >= 0 && c < C) *reinterpret_cast<uint4*>(grads + c * P + i) = v;
@@ -56,11 +56,11 @@ __global__ __launch_bounds__(256) void replica_fold_kernel(bf16_t* __restrict__ 
         continue;
       }
       if (slot_tokens != nullptr && slot_tokens[c] <= 0) continue;
-      acc += bf16_to_f32(grads[c * P + i]);
+      acc += E::to_f32(grads[c * P + i]);
     }
     out[e * P + i] = acc;
     if (writeback) {
-      const bf16_t v = (bf16_t)f32_to_bf16(acc);
+      const bf16_t v = (bf16_t)E::from_f32(acc);
       for (int32_t j = b; j < end; ++j) {
         const int64_t c = copy_slots[j];
         if (c >= 0 && c < C) grads[c * P + i] = v;
@@ -70,11 +70,12 @@ __global__ __launch_bounds__(256) void replica_fold_kernel(bf16_t* __restrict__ 
   if (bad && status != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *status = 1;
 }
 
-}  // namespace
 
-extern "C" int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const int32_t* copy_slots,
-                                const int64_t* slot_tokens, int32_t E, int32_t C, int64_t P, float* out,
-                                int32_t writeback, int32_t* status, pmx_stream_t stream) {
+// El: the element type of the copies' gradients.
+template <class El>
+int replica_fold_t(void* grads, const int32_t* copy_offsets, const int32_t* copy_slots, const int64_t* slot_tokens,
+                   int32_t E, int32_t C, int64_t P, float* out, int32_t writeback, int32_t* status,
+                   pmx_stream_t stream) {
   if (E <= 0 || C <= 0 || P < 0 || E > 65535) return PMX_ERR_ARG;
   if (P == 0) return PMX_OK;
   if (!grads || !copy_offsets || !copy_slots || !out) return PMX_ERR_ARG;
@@ -85,12 +86,29 @@ extern "C" int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const 
   if (gx > 0x7fffffff) return PMX_ERR_SHAPE;
   dim3 grid((unsigned)gx, (unsigned)E);
   if (vec) {
-    replica_fold_kernel<true><<<grid, 256, 0, stream>>>(static_cast<bf16_t*>(grads), copy_offsets, copy_slots,
-                                                       slot_tokens, C, P, out, writeback, status);
-  } else {
-    replica_fold_kernel<false><<<grid, 256, 0, stream>>>(static_cast<bf16_t*>(grads), copy_offsets, copy_slots,
+    replica_fold_kernel<El, true><<<grid, 256, 0, stream>>>(static_cast<bf16_t*>(grads), copy_offsets, copy_slots,
                                                         slot_tokens, C, P, out, writeback, status);
+  } else {
+    replica_fold_kernel<El, false><<<grid, 256, 0, stream>>>(static_cast<bf16_t*>(grads), copy_offsets, copy_slots,
+                                                         slot_tokens, C, P, out, writeback, status);
   }
   PMX_LAUNCH_CHECK();
   return PMX_OK;
 }
+
+}  // namespace
+
+extern "C" int pmx_replica_fold(void* grads, const int32_t* copy_offsets, const int32_t* copy_slots,
+                                const int64_t* slot_tokens, int32_t E, int32_t C, int64_t P, float* out,
+                                int32_t writeback, int32_t* status, pmx_stream_t stream) {
+  return replica_fold_t<EltBF16>(grads, copy_offsets, copy_slots, slot_tokens, E, C, P, out, writeback, status,
+                                stream);
+}
+
+extern "C" int pmx_replica_fold_f16(void* grads, const int32_t* copy_offsets, const int32_t* copy_slots,
+                                    const int64_t* slot_tokens, int32_t E, int32_t C, int64_t P, float* out,
+                                    int32_t writeback, int32_t* status, pmx_stream_t stream) {
+  return replica_fold_t<EltF16>(grads, copy_offsets, copy_slots, slot_tokens, E, C, P, out, writeback, status,
+                                stream);
+}
+

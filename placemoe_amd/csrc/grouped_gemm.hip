@@ -38,7 +38,43 @@
 #include "common.h"
 #include "ktile.h"
 
+// Element type of this build of the file: bf16, or fp16 with -DPMX_ELT_F16
+// (the C-ABI entry points then carry the suffix _f16).  Both builds share
+// every kernel; only the MFMA instruction and the fp32 conversions differ.
+#ifdef PMX_ELT_F16
+#define PMX_GEMM_FN(name) name##_f16
+#else
+#define PMX_GEMM_FN(name) name
+#endif
+
 namespace {
+
+#ifdef PMX_ELT_F16
+using Elt = EltF16;
+#else
+using Elt = EltBF16;
+#endif
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// The MFMAs of the element type; fragments hold the 16-bit patterns as
+// bf16x8_t either way (the LDS reads move bits).
+__device__ __forceinline__ f32x16_t mfma32(const bf16x8_t& b, const bf16x8_t& a, const f32x16_t& c) {
+#ifdef PMX_ELT_F16
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, b), __builtin_bit_cast(f16x8_t, a), c, 0,
+                                                 0, 0);
+#else
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0);
+#endif
+}
+__device__ __forceinline__ f32x4_t mfma16(const bf16x8_t& b, const bf16x8_t& a, const f32x4_t& c) {
+#ifdef PMX_ELT_F16
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, b), __builtin_bit_cast(f16x8_t, a), c, 0,
+                                                 0, 0);
+#else
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(b, a, c, 0, 0, 0);
+#endif
+}
 
 // K-tiles are 64 deep so that every K-contiguous row segment a load
 // instruction fetches is one whole 128-byte line: with 32-deep K-tiles each
@@ -421,8 +457,7 @@ template <int BM, int I, int N, bool FIRST = false>
 __device__ __forceinline__ void mma_some(const Frags<BM>& f, f32x16_t (&acc)[MT][NTT]) {
 #pragma unroll
   for (int x = I; x < I + N; ++x)
-    acc[x / NTT][x % NTT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        f.b[x % NTT], f.a[x / NTT], FIRST ? f32x16_t{} : acc[x / NTT][x % NTT], 0, 0, 0);
+    acc[x / NTT][x % NTT] = mfma32(f.b[x % NTT], f.a[x / NTT], FIRST ? f32x16_t{} : acc[x / NTT][x % NTT]);
 }
 
 template <int BM>
@@ -431,7 +466,7 @@ __device__ __forceinline__ void mma_frags(const Frags<BM>& f, f32x16_t (&acc)[MT
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int nt = 0; nt < NTT; ++nt)
-      acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[nt], f.a[mt], acc[mt][nt], 0, 0, 0);
+      acc[mt][nt] = mfma32(f.b[nt], f.a[mt], acc[mt][nt]);
 }
 
 // Compile-time loop: f(Int<I>{}) for I = B .. E-1, so that accumulator
@@ -465,7 +500,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 // wave issues its next loads.  Rows of a round are 128 bytes; 16-byte chunk c
 // of row r sits at c ^ ((r >> 1) & 7).
 
-__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) { return make_uint2(pack2(a, b), pack2(c, d)); }
+__device__ __forceinline__ uint2 pack4(float a, float b, float c, float d) { return make_uint2(Elt::pack2(a, b), Elt::pack2(c, d)); }
 __device__ __forceinline__ uint2 acc4(const f32x16_t& a, int i) { return pack4(a[i], a[i + 1], a[i + 2], a[i + 3]); }
 
 // Byte offset, inside the stage, of byte `x` of row r (0..63) of the wave's staging area.
@@ -548,7 +583,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
         const int r = (q >> 3) * 64 + (q & 7) * 8 + (lane >> 3);
         const int32_t tok = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(rt, (uint32_t)r * 4u, 0, 0);
         dst[q] = r < nrows ? tok : -1;
-        if constexpr (KIND == KIND_NT) wt[q] = bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rw, (uint32_t)r * 2u, 0, 0));
+        if constexpr (KIND == KIND_NT) wt[q] = Elt::to_f32(__builtin_amdgcn_raw_buffer_load_b16(rw, (uint32_t)r * 2u, 0, 0));
       }
     }
   }
@@ -575,10 +610,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
         for (int k = 0; k < 4; k += 2) {
           g[k] = acc[mt][0][i + k], g[k + 1] = acc[mt][0][i + k + 1];
           u[k] = acc[mt][1][i + k], u[k + 1] = acc[mt][1][i + k + 1];
-          round2_bf16(g[k], g[k + 1]);
-          round2_bf16(u[k], u[k + 1]);
+          Elt::round2(g[k], g[k + 1]);
+          Elt::round2(u[k], u[k + 1]);
           g[k] = silu_f32(g[k]), g[k + 1] = silu_f32(g[k + 1]);
-          round2_bf16(g[k], g[k + 1]);
+          Elt::round2(g[k], g[k + 1]);
         }
         return pack4(g[0] * u[0], g[1] * u[1], g[2] * u[2], g[3] * u[3]);
       });
@@ -614,12 +649,12 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
       for (int q = 0; q < 8; ++q) {
         const uint4 v = staged_chunk(stage, wave, q * 8 + (lane >> 3), cc);
         float d[8], g[8], u[8], dg[8], du[8];
-        unpack8(v, d);
-        unpack8(gv[q], g);
-        unpack8(uv[q], u);
-        swiglu_bwd8(d, g, u, dg, du);
-        win_store(wo, vg, q * 8, pack8(dg));
-        win_store(wo, vu, q * 8, pack8(du));
+        unpack8e<Elt>(v, d);
+        unpack8e<Elt>(gv[q], g);
+        unpack8e<Elt>(uv[q], u);
+        swiglu_bwd8<Elt>(d, g, u, dg, du);
+        win_store(wo, vg, q * 8, pack8e<Elt>(dg));
+        win_store(wo, vu, q * 8, pack8e<Elt>(du));
       }
     } else if constexpr (KIND == KIND_TN) {
       stage_half<NTT>(stage, wave, lane, half, [&](int mt, int nt, int i) { return acc4(acc[mt][nt], i); });
@@ -657,10 +692,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
             win_store(wd, vd, 0, v);
           } else {
             float f[8];
-            unpack8(v, f);
+            unpack8e<Elt>(v, f);
 #pragma unroll
             for (int j = 0; j < 8; ++j) f[j] = __builtin_fmaf(f[j], wt[half * 8 + q], 0.f);
-            win_store(wd, vd, 0, pack8(f));
+            win_store(wd, vd, 0, pack8e<Elt>(f));
           }
         } else if ((KIND == KIND_NT || KIND == KIND_NN) && mapped && col < P.N && (uint32_t)d < (uint32_t)P.M) {
           if (KIND == KIND_NN) {
@@ -671,10 +706,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
             // f * w + 0 is the product's, with -0 made +0, and pack8 rounds
             // it to bf16.
             float f[8];
-            unpack8(v, f);
+            unpack8e<Elt>(v, f);
 #pragma unroll
             for (int j = 0; j < 8; ++j) f[j] = __builtin_fmaf(f[j], wt[half * 8 + q], 0.f);
-            st_stream(P.cout + (int64_t)d * P.ldc + col, pack8(f));
+            st_stream(P.cout + (int64_t)d * P.ldc + col, pack8e<Elt>(f));
           }
         }
       }
@@ -1646,8 +1681,7 @@ template <int I, int N, bool FIRST = false>
 __device__ __forceinline__ void mfma(const Frags& f, f32x4_t (&acc)[FM][FN]) {
 #pragma unroll
   for (int x = I; x < I + N; ++x)
-    acc[x / FN][x % FN] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.b[x % FN], f.a[x / FN],
-                                                                   FIRST ? f32x4_t{} : acc[x / FN][x % FN], 0, 0, 0);
+    acc[x / FN][x % FN] = mfma16(f.b[x % FN], f.a[x / FN], FIRST ? f32x4_t{} : acc[x / FN][x % FN]);
 }
 
 // Epilogue staging: a round is 64 of the wave's 128 rows; row r (0 .. 63) is
@@ -1683,7 +1717,7 @@ __device__ __forceinline__ uint4 staged(const char* stage, int wave, int r, int 
   return *reinterpret_cast<const uint4*>(stage + stg_off(wave, r, c));
 }
 
-__device__ __forceinline__ uint2 bf16x4(const f32x4_t& a) { return make_uint2(pack2(a[0], a[1]), pack2(a[2], a[3])); }
+__device__ __forceinline__ uint2 bf16x4(const f32x4_t& a) { return make_uint2(Elt::pack2(a[0], a[1]), Elt::pack2(a[2], a[3])); }
 
 // Write out the wave's 128 x 128 share of a finished tile (two rounds of 64
 // rows), with the kind's epilogue arithmetic - the same rounding points as
@@ -1749,10 +1783,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
         for (int e = 0; e < 4; e += 2) {
           g[e] = acc[mt][ng][e], g[e + 1] = acc[mt][ng][e + 1];
           u[e] = acc[mt][ng + 2][e], u[e + 1] = acc[mt][ng + 2][e + 1];
-          round2_bf16(g[e], g[e + 1]);
-          round2_bf16(u[e], u[e + 1]);
+          Elt::round2(g[e], g[e + 1]);
+          Elt::round2(u[e], u[e + 1]);
           g[e] = silu_f32(g[e]), g[e + 1] = silu_f32(g[e + 1]);
-          round2_bf16(g[e], g[e + 1]);
+          Elt::round2(g[e], g[e + 1]);
         }
         return pack4(g[0] * u[0], g[1] * u[1], g[2] * u[2], g[3] * u[3]);
       }, [](int k) { return k; });
@@ -1804,12 +1838,12 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
           const int r = qr * 16 + q * 4;
           const uint4 v = staged(stage, wave, r + rq, cc);
           float d[8], g[8], u[8], dg[8], du[8];
-          unpack8(v, d);
-          unpack8(nns_g[qq & 1][q], g);
-          unpack8(nns_u[qq & 1][q], u);
-          swiglu_bwd8(d, g, u, dg, du);
-          win_store(wo, vg, r, pack8(dg));
-          win_store(wo, vu, r, pack8(du));
+          unpack8e<Elt>(v, d);
+          unpack8e<Elt>(nns_g[qq & 1][q], g);
+          unpack8e<Elt>(nns_u[qq & 1][q], u);
+          swiglu_bwd8<Elt>(d, g, u, dg, du);
+          win_store(wo, vg, r, pack8e<Elt>(dg));
+          win_store(wo, vu, r, pack8e<Elt>(du));
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -1855,17 +1889,17 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
         const uint4 v = staged(stage, wave, q * 4 + rq, cc);
         if (!(KIND == KIND_NN && mapped)) win_store(w, voff, q * 4, v);
         const int32_t d = mapped ? __shfl(tok2[round], q * 4 + rq, 64) : -1;
-        const float wq = KIND == KIND_NT && mapped ? bf16_to_f32((uint32_t)__shfl((int32_t)wt2[round], q * 4 + rq, 64)) : 0.f;
+        const float wq = KIND == KIND_NT && mapped ? Elt::to_f32((uint32_t)__shfl((int32_t)wt2[round], q * 4 + rq, 64)) : 0.f;
         if ((KIND == KIND_NT || KIND == KIND_NN) && mapped && whole) {
           const uint32_t vd = col < P.N && (uint32_t)d < (uint32_t)P.M ? (uint32_t)d * wd.rowb + (uint32_t)col * 2u : kOOB;
           if (KIND == KIND_NN) {
             win_store(wd, vd, 0, v);
           } else {
             float f[8];
-            unpack8(v, f);
+            unpack8e<Elt>(v, f);
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = __builtin_fmaf(f[e], wq, 0.f);
-            win_store(wd, vd, 0, pack8(f));
+            win_store(wd, vd, 0, pack8e<Elt>(f));
           }
         } else if ((KIND == KIND_NT || KIND == KIND_NN) && mapped && col < P.N && (uint32_t)d < (uint32_t)P.M) {
           if (KIND == KIND_NN) {
@@ -1873,10 +1907,10 @@ __device__ __forceinline__ void epilogue(const GemmParams& P, const TileInfo& ti
           } else {
             // the combine kernel's rounding: 0 + bf16(f * w), as fma(f, w, 0)
             float f[8];
-            unpack8(v, f);
+            unpack8e<Elt>(v, f);
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = __builtin_fmaf(f[e], wq, 0.f);
-            st_stream(P.cout + (int64_t)d * P.ldc + col, pack8(f));
+            st_stream(P.cout + (int64_t)d * P.ldc + col, pack8e<Elt>(f));
           }
         }
         if (q % 8 == 7) __builtin_amdgcn_sched_barrier(0);
@@ -2232,7 +2266,7 @@ RowSrc one(const void* p, int64_t gs, int64_t ld) {
 
 extern "C" {
 
-int pmx_gemm_fc1_swiglu_fwd(const void* X, const void* w_gate, const void* w_up, int64_t w_copy_stride,
+int PMX_GEMM_FN(pmx_gemm_fc1_swiglu_fwd)(const void* X, const void* w_gate, const void* w_up, int64_t w_copy_stride,
                             const int32_t* offsets, int32_t G, int64_t A, int64_t H, int64_t I, void* gu,
                             void* act, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || A < 0 || H <= 0 || I <= 0) return PMX_ERR_ARG;
@@ -2258,12 +2292,12 @@ int pmx_gemm_fc1_swiglu_fwd(const void* X, const void* w_gate, const void* w_up,
   return launch<KIND_FC1>(P, stream);
 }
 
-int pmx_group_gemm_nt(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
+int PMX_GEMM_FN(pmx_group_gemm_nt)(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
                       int64_t K, void* C, pmx_stream_t stream) {
-  return pmx_group_gemm_nt_combine_top1(A, B, offsets, G, M, N, K, C, nullptr, nullptr, nullptr, stream);
+  return PMX_GEMM_FN(pmx_group_gemm_nt_combine_top1)(A, B, offsets, G, M, N, K, C, nullptr, nullptr, nullptr, stream);
 }
 
-int pmx_group_gemm_nt_combine_top1(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M,
+int PMX_GEMM_FN(pmx_group_gemm_nt_combine_top1)(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t M,
                                    int64_t N, int64_t K, void* C, const int32_t* row_token,
                                    const void* row_weight, void* out, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || M < 0 || N <= 0 || K <= 0) return PMX_ERR_ARG;
@@ -2293,14 +2327,14 @@ int pmx_group_gemm_nt_combine_top1(const void* A, const void* B, const int32_t* 
   return launch<KIND_NT>(P, stream);
 }
 
-int pmx_group_gemm_nn(const void* A, const void* B0, const void* B1, int64_t b_copy_stride, int64_t b_split,
+int PMX_GEMM_FN(pmx_group_gemm_nn)(const void* A, const void* B0, const void* B1, int64_t b_copy_stride, int64_t b_split,
                       const int32_t* offsets, int32_t G, int64_t M, int64_t N, int64_t K, void* C,
                       pmx_stream_t stream) {
-  return pmx_group_gemm_nn_unpermute_top1(A, B0, B1, b_copy_stride, b_split, offsets, G, M, N, K, nullptr, C,
+  return PMX_GEMM_FN(pmx_group_gemm_nn_unpermute_top1)(A, B0, B1, b_copy_stride, b_split, offsets, G, M, N, K, nullptr, C,
                                           stream);
 }
 
-int pmx_group_gemm_nn_unpermute_top1(const void* A, const void* B0, const void* B1, int64_t b_copy_stride,
+int PMX_GEMM_FN(pmx_group_gemm_nn_unpermute_top1)(const void* A, const void* B0, const void* B1, int64_t b_copy_stride,
                                      int64_t b_split, const int32_t* offsets, int32_t G, int64_t M, int64_t N,
                                      int64_t K, const int32_t* row_token, void* C, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || M < 0 || N <= 0 || K <= 0) return PMX_ERR_ARG;
@@ -2329,7 +2363,7 @@ int pmx_group_gemm_nn_unpermute_top1(const void* A, const void* B0, const void* 
   return launch<KIND_NN>(P, stream);
 }
 
-int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void* gu, const int32_t* offsets,
+int PMX_GEMM_FN(pmx_gemm_fc2_dgrad_swiglu_bwd)(const void* dY, const void* w_down, const void* gu, const int32_t* offsets,
                                   int32_t G, int64_t A, int64_t H, int64_t I, void* dG1, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || A < 0 || H <= 0 || I <= 0) return PMX_ERR_ARG;
   if (H % 8 || I % 8 || A > INT32_MAX) return PMX_ERR_SHAPE;  // row offsets are int32
@@ -2352,7 +2386,7 @@ int pmx_gemm_fc2_dgrad_swiglu_bwd(const void* dY, const void* w_down, const void
   return launch<KIND_NNS>(P, stream);
 }
 
-int pmx_group_gemm_tn(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t K, int64_t M,
+int PMX_GEMM_FN(pmx_group_gemm_tn)(const void* A, const void* B, const int32_t* offsets, int32_t G, int64_t K, int64_t M,
                       int64_t N, void* C0, void* C1, int64_t c_copy_stride, int64_t c_split, pmx_stream_t stream) {
   if (G <= 0 || G > kMaxGroups || K < 0 || M <= 0 || N <= 0) return PMX_ERR_ARG;
   if (M % 8 || N % 8) return PMX_ERR_SHAPE;

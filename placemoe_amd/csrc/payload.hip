@@ -216,6 +216,7 @@ __global__ __launch_bounds__(kScanBlock) void run_offsets_kernel(const int32_t* 
 
 // out[run] = bf16( sum_{a in run} fp32( bf16(Y[pos[a]] * w[a]) ) ); one block
 // per potential run start (blocks past the number of runs exit).
+template <class E>
 __global__ __launch_bounds__(256) void run_combine_kernel(const bf16_t* __restrict__ Y,
                                                           const int32_t* __restrict__ pos,
                                                           const bf16_t* __restrict__ w,
@@ -230,12 +231,12 @@ __global__ __launch_bounds__(256) void run_combine_kernel(const bf16_t* __restri
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int32_t a = b; a < e; ++a) {
       float f[8];
-      unpack8(ld_stream(reinterpret_cast<const uint4*>(Y + (int64_t)pos[a] * H) + i), f);
-      const float wk = bf16_to_f32(w[a]);
+      unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(Y + (int64_t)pos[a] * H) + i), f);
+      const float wk = E::to_f32(w[a]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += round_bf16(f[j] * wk);
+      for (int j = 0; j < 8; ++j) acc[j] += E::round(f[j] * wk);
     }
-    reinterpret_cast<uint4*>(out + run * H)[i] = pack8(acc);
+    reinterpret_cast<uint4*>(out + run * H)[i] = pack8e<E>(acc);
   }
 }
 
@@ -327,7 +328,12 @@ size_t pmx_ep_combine_workspace_bytes(int64_t num_recv) {
   return align256((size_t)num_recv * sizeof(int32_t)) + align256((size_t)nblocks * sizeof(int32_t)) + 256;
 }
 
-int pmx_ep_combine_aggregate(const void* Y, const int32_t* pos, const void* w, const int32_t* src_rank,
+}  // extern "C"
+
+namespace {
+
+template <class E>
+int ep_combine_aggregate_t(const void* Y, const int32_t* pos, const void* w, const int32_t* src_rank,
                              const int32_t* src_token, int64_t N, int64_t H, int32_t R, void* out,
                              int32_t* run_offsets, int32_t* rank_runs, int32_t* num_runs, int32_t* status,
                              void* workspace, size_t workspace_bytes, pmx_stream_t stream) {
@@ -360,12 +366,33 @@ int pmx_ep_combine_aggregate(const void* Y, const int32_t* pos, const void* w, c
                                                                    run_offsets, rank_runs, status);
   PMX_LAUNCH_CHECK();
   if (H > 0) {
-    run_combine_kernel<<<(unsigned)N, 256, 0, stream>>>(static_cast<const bf16_t*>(Y), pos,
+    run_combine_kernel<E><<<(unsigned)N, 256, 0, stream>>>(static_cast<const bf16_t*>(Y), pos,
                                                         static_cast<const bf16_t*>(w), run_offsets, num_runs, H,
                                                         static_cast<bf16_t*>(out));
     PMX_LAUNCH_CHECK();
   }
   return PMX_OK;
 }
+
+}  // namespace
+
+extern "C" {
+
+int pmx_ep_combine_aggregate(const void* Y, const int32_t* pos, const void* w, const int32_t* src_rank,
+                             const int32_t* src_token, int64_t N, int64_t H, int32_t R, void* out,
+                             int32_t* run_offsets, int32_t* rank_runs, int32_t* num_runs, int32_t* status,
+                             void* workspace, size_t workspace_bytes, pmx_stream_t stream) {
+  return ep_combine_aggregate_t<EltBF16>(Y, pos, w, src_rank, src_token, N, H, R, out, run_offsets, rank_runs,
+                                        num_runs, status, workspace, workspace_bytes, stream);
+}
+
+int pmx_ep_combine_aggregate_f16(const void* Y, const int32_t* pos, const void* w, const int32_t* src_rank,
+                                 const int32_t* src_token, int64_t N, int64_t H, int32_t R, void* out,
+                                 int32_t* run_offsets, int32_t* rank_runs, int32_t* num_runs, int32_t* status,
+                                 void* workspace, size_t workspace_bytes, pmx_stream_t stream) {
+  return ep_combine_aggregate_t<EltF16>(Y, pos, w, src_rank, src_token, N, H, R, out, run_offsets, rank_runs,
+                                        num_runs, status, workspace, workspace_bytes, stream);
+}
+
 
 }  // extern "C"

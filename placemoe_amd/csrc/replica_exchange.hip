@@ -19,18 +19,26 @@
 
 namespace {
 
+// Element types of the exchanged gradients, by tag: EltBF16 and EltF16
+// (16-bit storage) or float; S is the storage type.
 template <typename T>
 struct Elem;
-template <>
-struct Elem<bf16_t> {
+template <class E16>
+struct Elem16 {
+  using S = bf16_t;
   static constexpr int kVec = 8;
-  __device__ static float load(const bf16_t* p) { return bf16_to_f32(*p); }
-  __device__ static void store(bf16_t* p, float v) { *p = (bf16_t)f32_to_bf16(v); }
-  __device__ static void load_vec(const bf16_t* p, float* f) { unpack8(ld_stream(p), f); }
-  __device__ static void store_vec(bf16_t* p, const float* f) { *reinterpret_cast<uint4*>(p) = pack8(f); }
+  __device__ static float load(const S* p) { return E16::to_f32(*p); }
+  __device__ static void store(S* p, float v) { *p = (S)E16::from_f32(v); }
+  __device__ static void load_vec(const S* p, float* f) { unpack8e<E16>(ld_stream(p), f); }
+  __device__ static void store_vec(S* p, const float* f) { *reinterpret_cast<uint4*>(p) = pack8e<E16>(f); }
 };
 template <>
+struct Elem<EltBF16> : Elem16<EltBF16> {};
+template <>
+struct Elem<EltF16> : Elem16<EltF16> {};
+template <>
 struct Elem<float> {
+  using S = float;
   static constexpr int kVec = 4;
   __device__ static float load(const float* p) { return *p; }
   __device__ static void store(float* p, float v) { *p = v; }
@@ -46,9 +54,9 @@ struct Elem<float> {
 
 // Adds elements [i, i + n) of `src` to acc[0 .. n).
 template <typename T>
-__device__ __forceinline__ void add_from(const T* src, int64_t i, int n, float* acc) {
+__device__ __forceinline__ void add_from(const typename Elem<T>::S* src, int64_t i, int n, float* acc) {
   constexpr int V = Elem<T>::kVec;
-  const T* p = src + i;
+  const typename Elem<T>::S* p = src + i;
   if (n == V && (reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
     float f[V];
     Elem<T>::load_vec(p, f);
@@ -60,9 +68,9 @@ __device__ __forceinline__ void add_from(const T* src, int64_t i, int n, float* 
 }
 
 template <typename T>
-__device__ __forceinline__ void store_to(T* dst, int64_t i, int n, const float* acc) {
+__device__ __forceinline__ void store_to(typename Elem<T>::S* dst, int64_t i, int n, const float* acc) {
   constexpr int V = Elem<T>::kVec;
-  T* p = dst + i;
+  typename Elem<T>::S* p = dst + i;
   if (n == V && (reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
     Elem<T>::store_vec(p, acc);
   } else {
@@ -71,7 +79,7 @@ __device__ __forceinline__ void store_to(T* dst, int64_t i, int n, const float* 
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void replica_items_kernel(T* __restrict__ grads, int64_t P, int32_t C,
+__global__ __launch_bounds__(256) void replica_items_kernel(typename Elem<T>::S* __restrict__ grads, int64_t P, int32_t C,
                                                             const int32_t* __restrict__ slot_offsets,
                                                             const int32_t* __restrict__ slots, int with_local,
                                                             int write_slots,
@@ -101,7 +109,7 @@ __global__ __launch_bounds__(256) void replica_items_kernel(T* __restrict__ grad
   }
   if (part_offsets != nullptr) {
     for (int32_t j = part_offsets[item]; j < part_offsets[item + 1]; ++j)
-      add_from<T>(reinterpret_cast<const T*>(part_ptrs[j]), i, n, acc);
+      add_from<T>(reinterpret_cast<const typename Elem<T>::S*>(part_ptrs[j]), i, n, acc);
   }
   if (write_slots) {
     for (int32_t j = s0; j < s1; ++j) {
@@ -111,7 +119,7 @@ __global__ __launch_bounds__(256) void replica_items_kernel(T* __restrict__ grad
   }
   if (out_offsets != nullptr) {
     for (int32_t j = out_offsets[item]; j < out_offsets[item + 1]; ++j)
-      store_to<T>(reinterpret_cast<T*>(out_ptrs[j]), i, n, acc);
+      store_to<T>(reinterpret_cast<typename Elem<T>::S*>(out_ptrs[j]), i, n, acc);
   }
 }
 
@@ -120,17 +128,21 @@ int launch_items(void* grads, int32_t dtype, int64_t P, int32_t C, int32_t n_ite
                  const int64_t* part_ptrs, const int32_t* out_offsets, const int64_t* out_ptrs, int32_t* status,
                  hipStream_t stream) {
   if (P < 0 || C < 0 || n_items < 0 || n_items > 65535) return PMX_ERR_ARG;
-  if (dtype != PMX_DTYPE_BF16 && dtype != PMX_DTYPE_F32) return PMX_ERR_ARG;
+  if (dtype != PMX_DTYPE_BF16 && dtype != PMX_DTYPE_F16 && dtype != PMX_DTYPE_F32) return PMX_ERR_ARG;
   if (P == 0 || n_items == 0) return PMX_OK;
   if (!slot_offsets || !status || ((with_local || write_slots) && (!grads || (C > 0 && !slots)))) return PMX_ERR_ARG;
   if ((part_offsets == nullptr) != (part_ptrs == nullptr) || (out_offsets == nullptr) != (out_ptrs == nullptr))
     return PMX_ERR_ARG;
-  const int V = dtype == PMX_DTYPE_BF16 ? 8 : 4;
+  const int V = dtype == PMX_DTYPE_F32 ? 4 : 8;
   const int64_t gx = (P + 256 * V - 1) / (256 * V);
   if (gx > 0x7fffffff) return PMX_ERR_SHAPE;
   const dim3 grid((unsigned)gx, (unsigned)n_items);
   if (dtype == PMX_DTYPE_BF16) {
-    replica_items_kernel<bf16_t><<<grid, 256, 0, stream>>>(static_cast<bf16_t*>(grads), P, C, slot_offsets, slots,
+    replica_items_kernel<EltBF16><<<grid, 256, 0, stream>>>(static_cast<bf16_t*>(grads), P, C, slot_offsets, slots,
+                                                            with_local, write_slots, part_offsets, part_ptrs,
+                                                            out_offsets, out_ptrs, status);
+  } else if (dtype == PMX_DTYPE_F16) {
+    replica_items_kernel<EltF16><<<grid, 256, 0, stream>>>(static_cast<bf16_t*>(grads), P, C, slot_offsets, slots,
                                                            with_local, write_slots, part_offsets, part_ptrs,
                                                            out_offsets, out_ptrs, status);
   } else {

@@ -401,7 +401,7 @@ __global__ __launch_bounds__(kRowThreads) void gather_rows_by_src_kernel(const b
 // out[t] = bf16( sum_k fp32(term_k) ), term_k = Y[pos] or bf16(Y[pos] * w).
 // KC > 0: K == KC at compile time; the K row loads of a chunk are issued
 // together, then summed in k order (the same order as the generic path).
-template <bool VEC, bool WEIGHTED, int KC = 0>
+template <class E, bool VEC, bool WEIGHTED, int KC = 0>
 __global__ __launch_bounds__(kRowThreads) void gather_rows_kernel(const bf16_t* __restrict__ Y,
                                                            const int32_t* __restrict__ pos,
                                                            const bf16_t* __restrict__ w, int32_t K,
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(kRowThreads) void gather_rows_kernel(const bf16_t* 
 #pragma unroll
     for (int k = 0; k < KC; ++k) {
       rows[k] = (int64_t)p[k] * H;
-      wk[k] = WEIGHTED ? bf16_to_f32(w[t * KC + k]) : 1.f;
+      wk[k] = WEIGHTED ? E::to_f32(w[t * KC + k]) : 1.f;
     }
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       uint4 v[KC];
@@ -425,11 +425,11 @@ __global__ __launch_bounds__(kRowThreads) void gather_rows_kernel(const bf16_t* 
 #pragma unroll
       for (int k = 0; k < KC; ++k) {
         float f[8];
-        unpack8(v[k], f);
+        unpack8e<E>(v[k], f);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += WEIGHTED ? round_bf16(f[j] * wk[k]) : f[j];
+        for (int j = 0; j < 8; ++j) acc[j] += WEIGHTED ? E::round(f[j] * wk[k]) : f[j];
       }
-      reinterpret_cast<uint4*>(out + t * H)[i] = pack8(acc);
+      reinterpret_cast<uint4*>(out + t * H)[i] = pack8e<E>(acc);
     }
   } else if (VEC) {
     const int64_t n8 = H / 8;
@@ -438,27 +438,27 @@ __global__ __launch_bounds__(kRowThreads) void gather_rows_kernel(const bf16_t* 
       for (int k = 0; k < K; ++k) {
         const uint4 v = ld_stream(reinterpret_cast<const uint4*>(Y + (int64_t)p[k] * H) + i);
         float f[8];
-        unpack8(v, f);
+        unpack8e<E>(v, f);
         if (WEIGHTED) {
-          const float wk = bf16_to_f32(w[t * K + k]);
+          const float wk = E::to_f32(w[t * K + k]);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[j] += round_bf16(f[j] * wk);
+          for (int j = 0; j < 8; ++j) acc[j] += E::round(f[j] * wk);
         } else {
 #pragma unroll
           for (int j = 0; j < 8; ++j) acc[j] += f[j];
         }
       }
-      reinterpret_cast<uint4*>(out + t * H)[i] = pack8(acc);
+      reinterpret_cast<uint4*>(out + t * H)[i] = pack8e<E>(acc);
     }
   } else {
     for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
       float acc = 0.f;
       for (int k = 0; k < K; ++k) {
-        const float f = bf16_to_f32(Y[(int64_t)p[k] * H + i]);
-        if (WEIGHTED) acc += round_bf16(f * bf16_to_f32(w[t * K + k]));
+        const float f = E::to_f32(Y[(int64_t)p[k] * H + i]);
+        if (WEIGHTED) acc += E::round(f * E::to_f32(w[t * K + k]));
         else acc += f;
       }
-      out[t * H + i] = (bf16_t)f32_to_bf16(acc);
+      out[t * H + i] = (bf16_t)E::from_f32(acc);
     }
   }
 }
@@ -467,7 +467,7 @@ __global__ __launch_bounds__(kRowThreads) void gather_rows_kernel(const bf16_t* 
 // Top-1 (KC == 1) stores dY with streaming stores (see st_row).  dout and Y
 // are read with streaming loads: plain loads measured 1.5-3% faster on
 // isolated buffers but 11% slower inside the layer step (Qwen3 shape).
-template <bool VEC, int KC = 0>
+template <class E, bool VEC, int KC = 0>
 __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* __restrict__ dout,
                                                            const bf16_t* __restrict__ Y,
                                                            const int32_t* __restrict__ pos,
@@ -487,11 +487,11 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* 
 #pragma unroll
     for (int k = 0; k < KC; ++k) {
       rows[k] = (int64_t)p[k] * H;
-      wk[k] = bf16_to_f32(w[t * KC + k]);
+      wk[k] = E::to_f32(w[t * KC + k]);
     }
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       float d[8];
-      unpack8(ld_stream(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
+      unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
       uint4 yv[KC];
 #pragma unroll
       for (int k = 0; k < KC; ++k) yv[k] = ld_stream(reinterpret_cast<const uint4*>(Y + rows[k]) + i);
@@ -500,11 +500,11 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* 
         float g[8], y[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) g[j] = d[j] * wk[k];
-        st_row<KC == 1>(reinterpret_cast<uint4*>(dY + rows[k]) + i, pack8(g));
-        unpack8(yv[k], y);
+        st_row<KC == 1>(reinterpret_cast<uint4*>(dY + rows[k]) + i, pack8e<E>(g));
+        unpack8e<E>(yv[k], y);
         float s = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s += round_bf16(d[j] * y[j]);
+        for (int j = 0; j < 8; ++j) s += E::round(d[j] * y[j]);
         part[k] += s;
       }
     }
@@ -512,34 +512,34 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* 
     const int64_t n8 = H / 8;
     for (int64_t i = threadIdx.x; i < n8; i += blockDim.x) {
       float d[8];
-      unpack8(ld_stream(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
+      unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(dout + t * H) + i), d);
 #pragma unroll
       for (int k = 0; k < kMaxTopK; ++k) {
         if (k < K) {
           const int64_t row = p[k];
-          const float wk = bf16_to_f32(w[t * K + k]);
+          const float wk = E::to_f32(w[t * K + k]);
           float g[8], y[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) g[j] = d[j] * wk;
-          reinterpret_cast<uint4*>(dY + row * H)[i] = pack8(g);
-          unpack8(ld_stream(reinterpret_cast<const uint4*>(Y + row * H) + i), y);
+          reinterpret_cast<uint4*>(dY + row * H)[i] = pack8e<E>(g);
+          unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(Y + row * H) + i), y);
           float s = 0.f;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) s += round_bf16(d[j] * y[j]);
+          for (int j = 0; j < 8; ++j) s += E::round(d[j] * y[j]);
           part[k] += s;
         }
       }
     }
   } else {
     for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
-      const float d = bf16_to_f32(dout[t * H + i]);
+      const float d = E::to_f32(dout[t * H + i]);
 #pragma unroll
       for (int k = 0; k < kMaxTopK; ++k) {
         if (k < K) {
           const int64_t row = p[k];
-          const float wk = bf16_to_f32(w[t * K + k]);
-          dY[row * H + i] = (bf16_t)f32_to_bf16(d * wk);
-          part[k] += round_bf16(d * bf16_to_f32(Y[row * H + i]));
+          const float wk = E::to_f32(w[t * K + k]);
+          dY[row * H + i] = (bf16_t)E::from_f32(d * wk);
+          part[k] += E::round(d * E::to_f32(Y[row * H + i]));
         }
       }
     }
@@ -557,7 +557,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* 
   if (threadIdx.x < (unsigned)K) {
     float s = 0.f;
     for (int wv = 0; wv < nwaves; ++wv) s += red[wv][threadIdx.x];
-    dw[t * K + threadIdx.x] = (bf16_t)f32_to_bf16(s);
+    dw[t * K + threadIdx.x] = (bf16_t)E::from_f32(s);
   }
 }
 
@@ -568,7 +568,7 @@ __global__ __launch_bounds__(kRowThreads) void combine_bwd_kernel(const bf16_t* 
 // UNR = 14 a 7168-wide row takes one pass (measured 5.61 TB/s against 5.48
 // with two passes of 7; 8 tokens per block or plain stores of dY were no
 // faster).
-template <int UNR>
+template <class E, int UNR>
 __global__ __launch_bounds__(256) void combine_bwd_top1_kernel(const bf16_t* __restrict__ dout,
                                                                const bf16_t* __restrict__ Y,
                                                                const int32_t* __restrict__ pos,
@@ -578,7 +578,7 @@ __global__ __launch_bounds__(256) void combine_bwd_top1_kernel(const bf16_t* __r
   const int64_t t = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (t >= T) return;
   const int64_t row = (int64_t)pos[t] * H;
-  const float wk = bf16_to_f32(w[t]);
+  const float wk = E::to_f32(w[t]);
   const int64_t n8 = H / 8;
   const uint4* d_row = reinterpret_cast<const uint4*>(dout + t * H);
   const uint4* y_row = reinterpret_cast<const uint4*>(Y + row);
@@ -599,20 +599,20 @@ __global__ __launch_bounds__(256) void combine_bwd_top1_kernel(const bf16_t* __r
       const int64_t i = base + 64 * u;
       if (i < n8) {
         float d[8], y[8], g[8];
-        unpack8(dv[u], d);
-        unpack8(yv[u], y);
+        unpack8e<E>(dv[u], d);
+        unpack8e<E>(yv[u], y);
 #pragma unroll
         for (int j = 0; j < 8; ++j) g[j] = d[j] * wk;
-        st_stream(g_row + i, pack8(g));
+        st_stream(g_row + i, pack8e<E>(g));
         float s = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s += round_bf16(d[j] * y[j]);
+        for (int j = 0; j < 8; ++j) s += E::round(d[j] * y[j]);
         part += s;
       }
     }
   }
   part = wave_sum(part);
-  if (lane == 0) dw[t] = (bf16_t)f32_to_bf16(part);
+  if (lane == 0) dw[t] = (bf16_t)E::from_f32(part);
 }
 
 // Top-1 combine gradient in the rows' storage order: wave r handles row r of
@@ -621,7 +621,7 @@ __global__ __launch_bounds__(256) void combine_bwd_top1_kernel(const bf16_t* __r
 // 5.8 TB/s against 5.2 TB/s for the token-order walk (combine_bwd_top1_kernel),
 // whose Y reads and dY writes jump between rows; results are bit-identical
 // (the same arithmetic per element and the same per-row sum order).
-template <int UNR>
+template <class E, int UNR>
 __global__ __launch_bounds__(256) void combine_bwd_top1_rows_kernel(const bf16_t* __restrict__ dout,
                                                                     const bf16_t* __restrict__ Y,
                                                                     const int32_t* __restrict__ row_token,
@@ -633,7 +633,7 @@ __global__ __launch_bounds__(256) void combine_bwd_top1_rows_kernel(const bf16_t
   if (r >= T) return;
   const int64_t t = row_token[r];
   const bool ok = t >= 0 && t < T;
-  const float wk = ok ? bf16_to_f32(w[t]) : 0.f;
+  const float wk = ok ? E::to_f32(w[t]) : 0.f;
   const int64_t n8 = H / 8;
   const uint4* d_row = reinterpret_cast<const uint4*>(dout + (ok ? t : 0) * H);
   const uint4* y_row = reinterpret_cast<const uint4*>(Y + r * H);
@@ -654,20 +654,20 @@ __global__ __launch_bounds__(256) void combine_bwd_top1_rows_kernel(const bf16_t
       const int64_t i = base + 64 * u;
       if (i < n8) {
         float d[8], y[8], g[8];
-        unpack8(dv[u], d);
-        unpack8(yv[u], y);
+        unpack8e<E>(dv[u], d);
+        unpack8e<E>(yv[u], y);
 #pragma unroll
         for (int j = 0; j < 8; ++j) g[j] = d[j] * wk;
-        st_stream(g_row + i, pack8(g));
+        st_stream(g_row + i, pack8e<E>(g));
         float s = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s += round_bf16(d[j] * y[j]);
+        for (int j = 0; j < 8; ++j) s += E::round(d[j] * y[j]);
         part += s;
       }
     }
   }
   part = wave_sum(part);
-  if (lane == 0 && ok) dw[t] = (bf16_t)f32_to_bf16(part);
+  if (lane == 0 && ok) dw[t] = (bf16_t)E::from_f32(part);
 }
 
 // order[pos[i]] = i : the inverse of the stable scatter index.
@@ -677,7 +677,7 @@ __global__ void invert_kernel(const int32_t* __restrict__ pos, int64_t N, int32_
 }
 
 // out[r] = sum_{j in [off[r], off[r+1])} src[order[j]]  (fp32, bf16 store).
-template <bool VEC>
+template <class E, bool VEC>
 __global__ __launch_bounds__(kRowThreads) void segment_rows_kernel(const bf16_t* __restrict__ src,
                                                            const int32_t* __restrict__ order,
                                                            const int32_t* __restrict__ off, int64_t H,
@@ -690,17 +690,17 @@ __global__ __launch_bounds__(kRowThreads) void segment_rows_kernel(const bf16_t*
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
       for (int32_t j = b; j < e; ++j) {
         float f[8];
-        unpack8(ld_stream(reinterpret_cast<const uint4*>(src + (int64_t)order[j] * H) + i), f);
+        unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(src + (int64_t)order[j] * H) + i), f);
 #pragma unroll
         for (int q = 0; q < 8; ++q) acc[q] += f[q];
       }
-      reinterpret_cast<uint4*>(out + r * H)[i] = pack8(acc);
+      reinterpret_cast<uint4*>(out + r * H)[i] = pack8e<E>(acc);
     }
   } else {
     for (int64_t i = threadIdx.x; i < H; i += blockDim.x) {
       float acc = 0.f;
-      for (int32_t j = b; j < e; ++j) acc += bf16_to_f32(src[(int64_t)order[j] * H + i]);
-      out[r * H + i] = (bf16_t)f32_to_bf16(acc);
+      for (int32_t j = b; j < e; ++j) acc += E::to_f32(src[(int64_t)order[j] * H + i]);
+      out[r * H + i] = (bf16_t)E::from_f32(acc);
     }
   }
 }
@@ -845,7 +845,12 @@ int pmx_moe_scatter_src(const void* X, const int32_t* pos, const void* w, int64_
   return PMX_OK;
 }
 
-int pmx_moe_gather(const void* Y, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* out,
+}  // extern "C"
+
+namespace {
+
+template <class E>
+int moe_gather_t(const void* Y, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* out,
                    pmx_stream_t stream) {
   if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
   if (!rows_fit(T, K)) return PMX_ERR_SHAPE;
@@ -854,19 +859,20 @@ int pmx_moe_gather(const void* Y, const int32_t* pos, int64_t T, int32_t K, int6
   const unsigned th = row_threads(H);
   if (H % 8 == 0 && aligned16(Y) && aligned16(out)) {
 #define PMX_GATHER(KC)                                                                                  \
-  gather_rows_kernel<true, false, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, nullptr, K, H, \
+  gather_rows_kernel<E, true, false, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, nullptr, K, H, \
                                                                      (bf16_t*)out)
     PMX_DISPATCH_K(K, PMX_GATHER);
 #undef PMX_GATHER
   } else {
-    gather_rows_kernel<false, false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, nullptr, K, H,
+    gather_rows_kernel<E, false, false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, nullptr, K, H,
                                                                     (bf16_t*)out);
   }
   PMX_LAUNCH_CHECK();
   return PMX_OK;
 }
 
-int pmx_combine_fwd(const void* Y, const int32_t* pos, const void* w, int64_t T, int32_t K, int64_t H,
+template <class E>
+int combine_fwd_t(const void* Y, const int32_t* pos, const void* w, int64_t T, int32_t K, int64_t H,
                     void* out, pmx_stream_t stream) {
   if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
   if (!rows_fit(T, K)) return PMX_ERR_SHAPE;
@@ -875,19 +881,20 @@ int pmx_combine_fwd(const void* Y, const int32_t* pos, const void* w, int64_t T,
   const unsigned th = row_threads(H);
   if (H % 8 == 0 && aligned16(Y) && aligned16(out)) {
 #define PMX_COMBINE(KC)                                                                               \
-  gather_rows_kernel<true, true, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, (const bf16_t*)w, \
+  gather_rows_kernel<E, true, true, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, (const bf16_t*)w, \
                                                                     K, H, (bf16_t*)out)
     PMX_DISPATCH_K(K, PMX_COMBINE);
 #undef PMX_COMBINE
   } else {
-    gather_rows_kernel<false, true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, (const bf16_t*)w,
+    gather_rows_kernel<E, false, true><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)Y, pos, (const bf16_t*)w,
                                                                    K, H, (bf16_t*)out);
   }
   PMX_LAUNCH_CHECK();
   return PMX_OK;
 }
 
-int pmx_combine_bwd_top1_rows(const void* dout, const void* Y, const int32_t* row_token, const void* w,
+template <class E>
+int combine_bwd_top1_rows_t(const void* dout, const void* Y, const int32_t* row_token, const void* w,
                               int64_t T, int64_t H, void* dY, void* dw, pmx_stream_t stream) {
   if (T < 0 || H < 0) return PMX_ERR_ARG;
   if (!rows_fit(T, 1)) return PMX_ERR_SHAPE;
@@ -896,13 +903,14 @@ int pmx_combine_bwd_top1_rows(const void* dout, const void* Y, const int32_t* ro
   if (H % 8 || !aligned16(dout) || !aligned16(Y) || !aligned16(dY)) return PMX_ERR_SHAPE;
   const int64_t blocks = (T + 3) / 4;  // a wave per row, 4 rows per block
   if (blocks > 0x7fffffff) return PMX_ERR_SHAPE;
-  combine_bwd_top1_rows_kernel<14><<<(unsigned)blocks, 256, 0, stream>>>(
+  combine_bwd_top1_rows_kernel<E, 14><<<(unsigned)blocks, 256, 0, stream>>>(
       (const bf16_t*)dout, (const bf16_t*)Y, row_token, (const bf16_t*)w, T, H, (bf16_t*)dY, (bf16_t*)dw);
   PMX_LAUNCH_CHECK();
   return PMX_OK;
 }
 
-int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const void* w, int64_t T,
+template <class E>
+int combine_bwd_t(const void* dout, const void* Y, const int32_t* pos, const void* w, int64_t T,
                     int32_t K, int64_t H, void* dY, void* dw, pmx_stream_t stream) {
   if (T < 0 || K <= 0 || H < 0) return PMX_ERR_ARG;
   if (K > kMaxTopK) return PMX_ERR_ARG;
@@ -914,19 +922,19 @@ int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const v
     // top-1 rows of at least 2048 columns: a wave per token (4 tokens per block)
     const int64_t blocks = (T + 3) / 4;
     if (blocks > 0x7fffffff) return PMX_ERR_SHAPE;
-    combine_bwd_top1_kernel<14><<<(unsigned)blocks, 256, 0, stream>>>(
+    combine_bwd_top1_kernel<E, 14><<<(unsigned)blocks, 256, 0, stream>>>(
         (const bf16_t*)dout, (const bf16_t*)Y, pos, (const bf16_t*)w, T, H, (bf16_t*)dY, (bf16_t*)dw);
     PMX_LAUNCH_CHECK();
     return PMX_OK;
   }
   if (H % 8 == 0 && aligned16(dout) && aligned16(Y) && aligned16(dY)) {
 #define PMX_COMBINE_BWD(KC)                                                                            \
-  combine_bwd_kernel<true, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos, \
+  combine_bwd_kernel<E, true, KC><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos, \
                                                               (const bf16_t*)w, K, H, (bf16_t*)dY, (bf16_t*)dw)
     PMX_DISPATCH_K(K, PMX_COMBINE_BWD);
 #undef PMX_COMBINE_BWD
   } else {
-    combine_bwd_kernel<false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos,
+    combine_bwd_kernel<E, false><<<(unsigned)T, th, 0, stream>>>((const bf16_t*)dout, (const bf16_t*)Y, pos,
                                                              (const bf16_t*)w, K, H, (bf16_t*)dY,
                                                              (bf16_t*)dw);
   }
@@ -934,17 +942,8 @@ int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const v
   return PMX_OK;
 }
 
-size_t pmx_segment_sum_workspace_bytes(int64_t num_src_rows, int64_t num_rows) {
-  if (num_src_rows < 0 || num_rows <= 0 || num_rows > kRouteMaxSlots) return 0;
-  const int64_t N = num_src_rows;
-  size_t b = route_ws_bytes(N, (int32_t)num_rows);
-  b = (b + 255) / 256 * 256;
-  // phys, pos, order: int32 [N] each; counts [R], offsets [R+1]
-  b += (size_t)(3 * N + 2 * num_rows + 1) * sizeof(int32_t) + 4 * 256;
-  return b;
-}
-
-int pmx_segment_sum(const void* source, const int64_t* index, int64_t N, int64_t H, int64_t num_rows,
+template <class E>
+int segment_sum_t(const void* source, const int64_t* index, int64_t N, int64_t H, int64_t num_rows,
                     void* out, void* workspace, size_t workspace_bytes, pmx_stream_t stream) {
   if (N < 0 || H < 0 || num_rows < 0) return PMX_ERR_ARG;
   if (num_rows == 0) return N == 0 ? PMX_OK : PMX_ERR_ARG;
@@ -975,14 +974,78 @@ int pmx_segment_sum(const void* source, const int64_t* index, int64_t N, int64_t
   if (H == 0) return PMX_OK;
   const unsigned th = row_threads(H);
   if (H % 8 == 0 && aligned16(source) && aligned16(out)) {
-    segment_rows_kernel<true><<<(unsigned)R, th, 0, stream>>>((const bf16_t*)source, order, offsets, H,
+    segment_rows_kernel<E, true><<<(unsigned)R, th, 0, stream>>>((const bf16_t*)source, order, offsets, H,
                                                              (bf16_t*)out);
   } else {
-    segment_rows_kernel<false><<<(unsigned)R, th, 0, stream>>>((const bf16_t*)source, order, offsets, H,
+    segment_rows_kernel<E, false><<<(unsigned)R, th, 0, stream>>>((const bf16_t*)source, order, offsets, H,
                                                               (bf16_t*)out);
   }
   PMX_LAUNCH_CHECK();
   return PMX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t pmx_segment_sum_workspace_bytes(int64_t num_src_rows, int64_t num_rows) {
+  if (num_src_rows < 0 || num_rows <= 0 || num_rows > kRouteMaxSlots) return 0;
+  const int64_t N = num_src_rows;
+  size_t b = route_ws_bytes(N, (int32_t)num_rows);
+  b = (b + 255) / 256 * 256;
+  // phys, pos, order: int32 [N] each; counts [R], offsets [R+1]
+  b += (size_t)(3 * N + 2 * num_rows + 1) * sizeof(int32_t) + 4 * 256;
+  return b;
+}
+
+int pmx_moe_gather(const void* Y, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* out,
+                   pmx_stream_t stream) {
+  return moe_gather_t<EltBF16>(Y, pos, T, K, H, out, stream);
+}
+
+int pmx_moe_gather_f16(const void* Y, const int32_t* pos, int64_t T, int32_t K, int64_t H, void* out,
+                       pmx_stream_t stream) {
+  return moe_gather_t<EltF16>(Y, pos, T, K, H, out, stream);
+}
+
+int pmx_combine_fwd(const void* Y, const int32_t* pos, const void* w, int64_t T, int32_t K, int64_t H,
+                    void* out, pmx_stream_t stream) {
+  return combine_fwd_t<EltBF16>(Y, pos, w, T, K, H, out, stream);
+}
+
+int pmx_combine_fwd_f16(const void* Y, const int32_t* pos, const void* w, int64_t T, int32_t K, int64_t H,
+                        void* out, pmx_stream_t stream) {
+  return combine_fwd_t<EltF16>(Y, pos, w, T, K, H, out, stream);
+}
+
+int pmx_combine_bwd_top1_rows(const void* dout, const void* Y, const int32_t* row_token, const void* w,
+                              int64_t T, int64_t H, void* dY, void* dw, pmx_stream_t stream) {
+  return combine_bwd_top1_rows_t<EltBF16>(dout, Y, row_token, w, T, H, dY, dw, stream);
+}
+
+int pmx_combine_bwd_top1_rows_f16(const void* dout, const void* Y, const int32_t* row_token, const void* w,
+                                  int64_t T, int64_t H, void* dY, void* dw, pmx_stream_t stream) {
+  return combine_bwd_top1_rows_t<EltF16>(dout, Y, row_token, w, T, H, dY, dw, stream);
+}
+
+int pmx_combine_bwd(const void* dout, const void* Y, const int32_t* pos, const void* w, int64_t T,
+                    int32_t K, int64_t H, void* dY, void* dw, pmx_stream_t stream) {
+  return combine_bwd_t<EltBF16>(dout, Y, pos, w, T, K, H, dY, dw, stream);
+}
+
+int pmx_combine_bwd_f16(const void* dout, const void* Y, const int32_t* pos, const void* w, int64_t T,
+                        int32_t K, int64_t H, void* dY, void* dw, pmx_stream_t stream) {
+  return combine_bwd_t<EltF16>(dout, Y, pos, w, T, K, H, dY, dw, stream);
+}
+
+int pmx_segment_sum(const void* source, const int64_t* index, int64_t N, int64_t H, int64_t num_rows,
+                    void* out, void* workspace, size_t workspace_bytes, pmx_stream_t stream) {
+  return segment_sum_t<EltBF16>(source, index, N, H, num_rows, out, workspace, workspace_bytes, stream);
+}
+
+int pmx_segment_sum_f16(const void* source, const int64_t* index, int64_t N, int64_t H, int64_t num_rows,
+                        void* out, void* workspace, size_t workspace_bytes, pmx_stream_t stream) {
+  return segment_sum_t<EltF16>(source, index, N, H, num_rows, out, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

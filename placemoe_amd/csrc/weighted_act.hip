@@ -20,7 +20,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // out[r, :] = bf16(act[r, :] * row_w[r]).  VEC: one thread per 16-byte chunk
 // (N a multiple of 8), grid-stride; else one thread per element.
-template <bool VEC>
+template <class E, bool VEC>
 __global__ __launch_bounds__(256) void weight_rows_kernel(const bf16_t* __restrict__ act,
                                                           const bf16_t* __restrict__ row_w, int64_t R, int64_t N,
                                                           bf16_t* __restrict__ out) {
@@ -29,26 +29,27 @@ __global__ __launch_bounds__(256) void weight_rows_kernel(const bf16_t* __restri
     const int64_t n8 = N / 8;
     const int64_t total = R * n8;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step) {
-      const float w = bf16_to_f32(row_w[e / n8]);
+      const float w = E::to_f32(row_w[e / n8]);
       float a[8];
-      unpack8(ld_stream(reinterpret_cast<const uint4*>(act) + e), a);
+      unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(act) + e), a);
 #pragma unroll
       for (int j = 0; j < 8; ++j) a[j] *= w;
-      reinterpret_cast<uint4*>(out)[e] = pack8(a);
+      reinterpret_cast<uint4*>(out)[e] = pack8e<E>(a);
     }
   } else {
     const int64_t total = R * N;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += step)
-      out[e] = (bf16_t)f32_to_bf16(bf16_to_f32(act[e]) * bf16_to_f32(row_w[e / N]));
+      out[e] = (bf16_t)E::from_f32(E::to_f32(act[e]) * E::to_f32(row_w[e / N]));
   }
 }
 
 // Scalar form of swiglu_bwd8 (same operations and rounding points).
+template <class E>
 __device__ __forceinline__ void swiglu_bwd1(float dact, float g, float u, float& dgate, float& dup) {
   const float sig = sigmoid_f32(g);
   const float gs = g * sig;
-  dgate = round_bf16(dact * u) * __builtin_fmaf(gs, 1.0f - sig, sig);
-  dup = round_bf16(gs) * dact;
+  dgate = E::round(dact * u) * __builtin_fmaf(gs, 1.0f - sig, sig);
+  dup = E::round(gs) * dact;
 }
 
 // One wave per row, four rows per block.  Row r reads d_act_w[r], act[r] and
@@ -56,7 +57,7 @@ __device__ __forceinline__ void swiglu_bwd1(float dact, float g, float u, float&
 // gradient dw[row_src[r]] (not written when row_src[r] lies outside [0, A)).
 // The row sum: each lane sums its chunks in order (8 products per chunk, in
 // column order), then the wave's lanes are summed by a butterfly.
-template <bool VEC>
+template <class E, bool VEC>
 __global__ __launch_bounds__(256) void swiglu_bwd_weighted_kernel(
     const bf16_t* __restrict__ daw, const bf16_t* __restrict__ gu, const bf16_t* __restrict__ act,
     const bf16_t* __restrict__ row_w, const int32_t* __restrict__ row_src, int64_t R, int64_t I, int64_t A,
@@ -64,7 +65,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_weighted_kernel(
   const int lane = threadIdx.x & 63;
   const int64_t r = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (r >= R) return;
-  const float w = bf16_to_f32(row_w[r]);
+  const float w = E::to_f32(row_w[r]);
   const bf16_t* d_row = daw + r * I;
   const bf16_t* a_row = act + r * I;
   const bf16_t* g_row = gu + r * 2 * I;
@@ -74,49 +75,47 @@ __global__ __launch_bounds__(256) void swiglu_bwd_weighted_kernel(
     const int64_t n8 = I / 8;
     for (int64_t i = lane; i < n8; i += 64) {
       float d[8], a[8], g[8], u[8], dact[8], dgate[8], dup[8];
-      unpack8(ld_stream(reinterpret_cast<const uint4*>(d_row) + i), d);
-      unpack8(ld_stream(reinterpret_cast<const uint4*>(a_row) + i), a);
-      unpack8(ld_stream(reinterpret_cast<const uint4*>(g_row) + i), g);
-      unpack8(ld_stream(reinterpret_cast<const uint4*>(g_row + I) + i), u);
+      unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(d_row) + i), d);
+      unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(a_row) + i), a);
+      unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(g_row) + i), g);
+      unpack8e<E>(ld_stream(reinterpret_cast<const uint4*>(g_row + I) + i), u);
       float s = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
         dact[j] = d[j] * w;
         dact[j + 1] = d[j + 1] * w;
-        round2_bf16(dact[j], dact[j + 1]);
+        E::round2(dact[j], dact[j + 1]);
         float p0 = a[j] * d[j], p1 = a[j + 1] * d[j + 1];
-        round2_bf16(p0, p1);
+        E::round2(p0, p1);
         s += p0;
         s += p1;
       }
       part += s;
-      swiglu_bwd8(dact, g, u, dgate, dup);
-      reinterpret_cast<uint4*>(o_row)[i] = pack8(dgate);
-      reinterpret_cast<uint4*>(o_row + I)[i] = pack8(dup);
+      swiglu_bwd8<E>(dact, g, u, dgate, dup);
+      reinterpret_cast<uint4*>(o_row)[i] = pack8e<E>(dgate);
+      reinterpret_cast<uint4*>(o_row + I)[i] = pack8e<E>(dup);
     }
   } else {
     for (int64_t j = lane; j < I; j += 64) {
-      const float d = bf16_to_f32(d_row[j]);
-      const float dact = round_bf16(d * w);
-      part += round_bf16(bf16_to_f32(a_row[j]) * d);
+      const float d = E::to_f32(d_row[j]);
+      const float dact = E::round(d * w);
+      part += E::round(E::to_f32(a_row[j]) * d);
       float dgate, dup;
-      swiglu_bwd1(dact, bf16_to_f32(g_row[j]), bf16_to_f32(g_row[I + j]), dgate, dup);
-      o_row[j] = (bf16_t)f32_to_bf16(dgate);
-      o_row[I + j] = (bf16_t)f32_to_bf16(dup);
+      swiglu_bwd1<E>(dact, E::to_f32(g_row[j]), E::to_f32(g_row[I + j]), dgate, dup);
+      o_row[j] = (bf16_t)E::from_f32(dgate);
+      o_row[I + j] = (bf16_t)E::from_f32(dup);
     }
   }
   part = wave_sum(part);
   if (lane == 0 && dw != nullptr) {
     const int64_t k = row_src[r];
-    if (k >= 0 && k < A) dw[k] = (bf16_t)f32_to_bf16(part);
+    if (k >= 0 && k < A) dw[k] = (bf16_t)E::from_f32(part);
   }
 }
 
-}  // namespace
 
-extern "C" {
-
-int pmx_weight_rows(const void* act, const void* row_w, int64_t R, int64_t N, void* out, pmx_stream_t stream) {
+template <class E>
+int weight_rows_t(const void* act, const void* row_w, int64_t R, int64_t N, void* out, pmx_stream_t stream) {
   if (R < 0 || N < 0) return PMX_ERR_ARG;
   if (R == 0 || N == 0) return PMX_OK;
   if (!act || !row_w || !out) return PMX_ERR_ARG;
@@ -126,14 +125,17 @@ int pmx_weight_rows(const void* act, const void* row_w, int64_t R, int64_t N, vo
   const int64_t blocks = (work + 255) / 256;
   const unsigned grid = (unsigned)(blocks < 16384 ? blocks : 16384);
   if (vec)
-    weight_rows_kernel<true><<<grid, 256, 0, stream>>>((const bf16_t*)act, (const bf16_t*)row_w, R, N, (bf16_t*)out);
+    weight_rows_kernel<E, true><<<grid, 256, 0, stream>>>((const bf16_t*)act, (const bf16_t*)row_w, R, N,
+                                                          (bf16_t*)out);
   else
-    weight_rows_kernel<false><<<grid, 256, 0, stream>>>((const bf16_t*)act, (const bf16_t*)row_w, R, N, (bf16_t*)out);
+    weight_rows_kernel<E, false><<<grid, 256, 0, stream>>>((const bf16_t*)act, (const bf16_t*)row_w, R, N,
+                                                           (bf16_t*)out);
   PMX_LAUNCH_CHECK();
   return PMX_OK;
 }
 
-int pmx_swiglu_bwd_weighted(const void* d_act_w, const void* gu, const void* act, const void* row_w,
+template <class E>
+int swiglu_bwd_weighted_t(const void* d_act_w, const void* gu, const void* act, const void* row_w,
                             const int32_t* row_src, int64_t R, int64_t I, int64_t A, void* dG1, void* dw,
                             pmx_stream_t stream) {
   if (R < 0 || I < 0 || A < 0) return PMX_ERR_ARG;
@@ -144,15 +146,41 @@ int pmx_swiglu_bwd_weighted(const void* d_act_w, const void* gu, const void* act
   const bool vec = I % 8 == 0 && aligned16(d_act_w) && aligned16(gu) && aligned16(act) && aligned16(dG1);
   const unsigned grid = (unsigned)((R + 3) / 4);
   if (vec)
-    swiglu_bwd_weighted_kernel<true><<<grid, 256, 0, stream>>>(
+    swiglu_bwd_weighted_kernel<E, true><<<grid, 256, 0, stream>>>(
         (const bf16_t*)d_act_w, (const bf16_t*)gu, (const bf16_t*)act, (const bf16_t*)row_w, row_src, R, I, A,
         (bf16_t*)dG1, (bf16_t*)dw);
   else
-    swiglu_bwd_weighted_kernel<false><<<grid, 256, 0, stream>>>(
+    swiglu_bwd_weighted_kernel<E, false><<<grid, 256, 0, stream>>>(
         (const bf16_t*)d_act_w, (const bf16_t*)gu, (const bf16_t*)act, (const bf16_t*)row_w, row_src, R, I, A,
         (bf16_t*)dG1, (bf16_t*)dw);
   PMX_LAUNCH_CHECK();
   return PMX_OK;
 }
+
+}  // namespace
+
+extern "C" {
+
+int pmx_weight_rows(const void* act, const void* row_w, int64_t R, int64_t N, void* out, pmx_stream_t stream) {
+  return weight_rows_t<EltBF16>(act, row_w, R, N, out, stream);
+}
+
+int pmx_weight_rows_f16(const void* act, const void* row_w, int64_t R, int64_t N, void* out, pmx_stream_t stream) {
+  return weight_rows_t<EltF16>(act, row_w, R, N, out, stream);
+}
+
+
+int pmx_swiglu_bwd_weighted(const void* d_act_w, const void* gu, const void* act, const void* row_w,
+                            const int32_t* row_src, int64_t R, int64_t I, int64_t A, void* dG1, void* dw,
+                            pmx_stream_t stream) {
+  return swiglu_bwd_weighted_t<EltBF16>(d_act_w, gu, act, row_w, row_src, R, I, A, dG1, dw, stream);
+}
+
+int pmx_swiglu_bwd_weighted_f16(const void* d_act_w, const void* gu, const void* act, const void* row_w,
+                                const int32_t* row_src, int64_t R, int64_t I, int64_t A, void* dG1, void* dw,
+                                pmx_stream_t stream) {
+  return swiglu_bwd_weighted_t<EltF16>(d_act_w, gu, act, row_w, row_src, R, I, A, dG1, dw, stream);
+}
+
 
 }  // extern "C"

@@ -22,6 +22,7 @@ import torch
 from . import _capi
 
 BF16 = torch.bfloat16
+HALF = (torch.bfloat16, torch.float16)
 
 
 def _stream(device: torch.device) -> ctypes.c_void_p:
@@ -38,7 +39,8 @@ def build_local_payload(hidden_states: torch.Tensor, selected_experts: torch.Ten
     ``num_experts // ep_size`` slots each; ``physical_experts`` (copy slots)
     replace ``selected_experts`` for the routing when given."""
     assert hidden_states.is_cuda, "placemoe_amd kernels need GPU tensors"
-    assert hidden_states.dtype == BF16, f"hidden_states must be bfloat16, got {hidden_states.dtype}"
+    assert hidden_states.dtype in HALF, f"hidden_states must be bfloat16 or float16, got {hidden_states.dtype}"
+    dt = hidden_states.dtype  # the payload copies 16-bit patterns: either type
     device = hidden_states.device
     num_local = num_experts // ep_size
     if num_local <= 0:
@@ -53,7 +55,7 @@ def build_local_payload(hidden_states: torch.Tensor, selected_experts: torch.Ten
     H = int(hidden_states.shape[-1])
     A = T * K
     phys = routed.to(device=device, dtype=torch.int32).contiguous()
-    weights = routing_weights.to(device=device, dtype=BF16).contiguous()
+    weights = routing_weights.to(device=device, dtype=dt).contiguous()
     hidden = hidden_states.contiguous()
     pad = (-H) % 8
     if pad:
@@ -65,10 +67,10 @@ def build_local_payload(hidden_states: torch.Tensor, selected_experts: torch.Ten
     assign_offsets = torch.empty(ep_size + 1, **i32)
     unique_counts = torch.empty(ep_size, **i32)
     unique_offsets = torch.empty(ep_size + 1, **i32)
-    send_hidden = torch.empty((A, Hp), dtype=BF16, device=device)
+    send_hidden = torch.empty((A, Hp), dtype=dt, device=device)
     unique_tokens = torch.empty(A, **i32)
     send_meta = torch.empty((A, 3), **i32)
-    send_weights = torch.empty(A, dtype=BF16, device=device)
+    send_weights = torch.empty(A, dtype=dt, device=device)
     target_rank = torch.empty(A, **i32)
     status = torch.zeros(1, **i32)
     ws = _workspace(_capi.load().pmx_ep_payload_workspace_bytes(A, ep_size), device)
@@ -101,9 +103,11 @@ def combine_aggregate(expert_outputs: torch.Tensor, pos: torch.Tensor, recv_weig
                       source_ranks: torch.Tensor, source_token_indices: torch.Tensor, ep_size: int):
     """Per (source rank, source token) fp32 sums of ``bf16(expert_outputs[pos[a]] * w[a])``
     over the received assignments ``a`` in receive order; returns the partial
-    rows [U, H] (bf16) and the rows per source rank (a host list)."""
+    rows [U, H] (in the outputs' dtype, bf16 or fp16, which also rounds the
+    products) and the rows per source rank (a host list)."""
     assert expert_outputs.is_cuda, "placemoe_amd kernels need GPU tensors"
-    assert expert_outputs.dtype == BF16, f"expert_outputs must be bfloat16, got {expert_outputs.dtype}"
+    assert expert_outputs.dtype in HALF, f"expert_outputs must be bfloat16 or float16, got {expert_outputs.dtype}"
+    dt = expert_outputs.dtype
     device = expert_outputs.device
     N = int(pos.numel())
     H = int(expert_outputs.shape[-1])
@@ -114,17 +118,18 @@ def combine_aggregate(expert_outputs: torch.Tensor, pos: torch.Tensor, recv_weig
     Hp = H + pad
     i32 = dict(dtype=torch.int32, device=device)
     pos32 = pos.to(**i32).contiguous()
-    w = recv_weights.reshape(-1).to(device=device, dtype=BF16).contiguous()
+    w = recv_weights.reshape(-1).to(device=device, dtype=dt).contiguous()
     ranks = source_ranks.to(**i32).contiguous()
     tokens = source_token_indices.to(**i32).contiguous()
-    out = torch.empty((max(N, 1), Hp), dtype=BF16, device=device)
+    out = torch.empty((max(N, 1), Hp), dtype=dt, device=device)
     run_offsets = torch.empty(N + 1, **i32)
     rank_runs = torch.empty(ep_size, **i32)
     num_runs = torch.empty(1, **i32)
     status = torch.zeros(1, **i32)
     ws = _workspace(_capi.load().pmx_ep_combine_workspace_bytes(N), device)
+    name = "pmx_ep_combine_aggregate_f16" if dt == torch.float16 else "pmx_ep_combine_aggregate"
     _capi.call(
-        "pmx_ep_combine_aggregate", y.data_ptr(), pos32.data_ptr() if N else None, w.data_ptr() if N else None,
+        name, y.data_ptr(), pos32.data_ptr() if N else None, w.data_ptr() if N else None,
         ranks.data_ptr() if N else None, tokens.data_ptr() if N else None, N, Hp, ep_size, out.data_ptr(),
         run_offsets.data_ptr(), rank_runs.data_ptr(), num_runs.data_ptr(), status.data_ptr(), ws.data_ptr(),
         ws.numel(), _stream(device),
@@ -151,7 +156,8 @@ def aggregate_weighted_outputs(weighted_outputs: torch.Tensor, source_token_indi
     ranks = torch.repeat_interleave(torch.arange(R, device=device),
                                     torch.as_tensor(split_sizes, device=device, dtype=torch.long))
     N = int(weighted_outputs.shape[0])
-    ones = torch.ones(N, dtype=BF16, device=device)
-    sums, splits = combine_aggregate(weighted_outputs.to(BF16), torch.arange(N, device=device), ones, ranks,
+    dt = weighted_outputs.dtype if weighted_outputs.dtype in HALF else BF16
+    ones = torch.ones(N, dtype=dt, device=device)
+    sums, splits = combine_aggregate(weighted_outputs.to(dt), torch.arange(N, device=device), ones, ranks,
                                      source_token_indices, R)
     return sums.to(weighted_outputs.dtype), splits

@@ -144,10 +144,14 @@ class _ExpertLayerBase(torch.autograd.Function):
         C, H2, inter = fc2_weight.shape
         assert H2 == H, f"down_proj hidden size {H2} != hidden size {H}"
         # fc1 must describe the same C copies, hidden size and intermediate size as fc2.
-        assert w_gate.dtype == torch.bfloat16 and w_up.dtype == torch.bfloat16, (
-            f"fc1 weights must be bfloat16, got {w_gate.dtype}/{w_up.dtype}"
+        # bf16 or fp16 throughout: the weights in the hidden states' dtype
+        assert hidden.dtype in (torch.bfloat16, torch.float16), (
+            f"hidden states must be bfloat16 or float16, got {hidden.dtype}"
         )
-        assert fc2_weight.dtype == torch.bfloat16, f"fc2 weight must be bfloat16, got {fc2_weight.dtype}"
+        assert w_gate.dtype == hidden.dtype and w_up.dtype == hidden.dtype, (
+            f"fc1 weights must be {hidden.dtype} like the hidden states, got {w_gate.dtype}/{w_up.dtype}"
+        )
+        assert fc2_weight.dtype == hidden.dtype, f"fc2 weight must be {hidden.dtype}, got {fc2_weight.dtype}"
         fc1_shape = (C, inter, H) if split else (C, 2 * inter, H)
         assert tuple(w_gate.shape) == fc1_shape, (
             f"fc1 weight shape {tuple(w_gate.shape)} does not match fc2 {tuple(fc2_weight.shape)} "

@@ -99,12 +99,12 @@ def hip_fused_moe_forward(
             raise ValueError("Provide either split fc1 weights or merged fc1_1_2_weight, not both.")
     elif fc1_1_weight is None or fc1_2_weight is None:
         raise ValueError("Split fc1 mode requires both fc1_1_weight and fc1_2_weight.")
-    if hidden_states.dtype != torch.bfloat16:
-        raise NotImplementedError(f"the hip fused MoE backend computes in bfloat16, got {hidden_states.dtype}")
     shape = hidden_states.shape
     hidden = hidden_states.reshape(-1, shape[-1]).contiguous()
     sel = selected_experts.reshape(hidden.shape[0], -1)
-    w = routing_weights.reshape(sel.shape).to(torch.bfloat16).contiguous()
+    # router weights in the hidden states' dtype (bf16 or fp16), which every
+    # rounding point of the layer then uses
+    w = routing_weights.reshape(sel.shape).to(hidden.dtype).contiguous()
     placement = PLACEMENTS.get(layer_key)
     mapping = sources = recorder = None
     source = 0

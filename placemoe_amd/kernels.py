@@ -16,6 +16,8 @@ import torch
 from . import _capi
 
 BF16 = torch.bfloat16
+F16 = torch.float16
+HALF = (BF16, F16)
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -38,9 +40,19 @@ def _check_dev(*tensors: torch.Tensor | None) -> torch.device:
     return dev
 
 
-def _bf16(name: str, t: torch.Tensor) -> None:
-    assert t.dtype == BF16, f"{name} must be bfloat16, got {t.dtype}"
+def _half(name: str, t: torch.Tensor, like: torch.dtype | None = None) -> torch.dtype:
+    """A 16-bit float operand: bfloat16 or float16, contiguous, and of the
+    dtype ``like`` of the call's other operands; returns its dtype."""
+    assert t.dtype in HALF, f"{name} must be bfloat16 or float16, got {t.dtype}"
+    if like is not None:
+        assert t.dtype == like, f"{name} must be {like} like the other operands, got {t.dtype}"
     assert t.is_contiguous(), f"{name} must be contiguous"
+    return t.dtype
+
+
+def _sym(name: str, dtype: torch.dtype) -> str:
+    """The entry point for the dtype: fp16 tensors go to the *_f16 twin."""
+    return name + "_f16" if dtype == F16 else name
 
 
 # ---------------------------------------------------------------------------
@@ -149,7 +161,7 @@ class RouteCheck:
 def moe_scatter(x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
     """Xp[pos[t,k]] = x[t]  ->  [T*K, H]."""
     dev = _check_dev(x, pos)
-    _bf16("x", x)
+    dt = _half("x", x)
     assert pos.dtype == torch.int32 and pos.is_contiguous()
     T, H = x.shape
     K = pos.shape[1]
@@ -163,7 +175,7 @@ def moe_scatter_src(x: torch.Tensor, pos: torch.Tensor, w: torch.Tensor | None =
     t*K + k (int32 [T*K]), and with the router weights ``w`` [T, K] each row's
     weight row_w[pos[t,k]] = w[t,k] -> (Xp, row_src, row_w or None)."""
     dev = _check_dev(x, pos, w)
-    _bf16("x", x)
+    dt = _half("x", x)
     assert pos.dtype == torch.int32 and pos.is_contiguous()
     T, H = x.shape
     K = pos.shape[1]
@@ -171,7 +183,7 @@ def moe_scatter_src(x: torch.Tensor, pos: torch.Tensor, w: torch.Tensor | None =
     src = torch.empty(T * K, dtype=torch.int32, device=dev)
     row_w = None
     if w is not None:
-        _bf16("routing weights", w)
+        _half("routing weights", w, dt)
         assert w.numel() == T * K, "routing weights: one per (token, k)"
         row_w = torch.empty(T * K, dtype=w.dtype, device=dev)
     _capi.call("pmx_moe_scatter_src", _ptr(x), _ptr(pos), _ptr(w), T, K, H, _ptr(out), _ptr(src), _ptr(row_w),
@@ -182,39 +194,40 @@ def moe_scatter_src(x: torch.Tensor, pos: torch.Tensor, w: torch.Tensor | None =
 def moe_gather(y: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
     """out[t] = bf16(sum_k fp32(y[pos[t,k]]))  ->  [T, H]."""
     dev = _check_dev(y, pos)
-    _bf16("y", y)
+    dt = _half("y", y)
     assert pos.dtype == torch.int32 and pos.is_contiguous()
     T, K = pos.shape
     H = y.shape[1]
     out = torch.empty((T, H), dtype=y.dtype, device=dev)
-    _capi.call("pmx_moe_gather", _ptr(y), _ptr(pos), T, K, H, _ptr(out), _stream(dev))
+    _capi.call(_sym("pmx_moe_gather", dt), _ptr(y), _ptr(pos), T, K, H, _ptr(out), _stream(dev))
     return out
 
 
 def combine_fwd(y: torch.Tensor, pos: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """out[t] = bf16(sum_k fp32(bf16(y[pos[t,k]] * w[t,k])))."""
     dev = _check_dev(y, pos, w)
-    _bf16("y", y)
-    _bf16("routing weights", w)
+    dt = _half("y", y)
+    _half("routing weights", w, dt)
     T, K = pos.shape
     H = y.shape[1]
     out = torch.empty((T, H), dtype=y.dtype, device=dev)
-    _capi.call("pmx_combine_fwd", _ptr(y), _ptr(pos), _ptr(w), T, K, H, _ptr(out), _stream(dev))
+    _capi.call(_sym("pmx_combine_fwd", dt), _ptr(y), _ptr(pos), _ptr(w), T, K, H, _ptr(out), _stream(dev))
     return out
 
 
 def combine_bwd(dout: torch.Tensor, y: torch.Tensor, pos: torch.Tensor, w: torch.Tensor):
     """(dy [T*K,H], dw [T,K]) - the gradients of ``combine_fwd``."""
     dev = _check_dev(dout, y, pos, w)
-    _bf16("grad_output", dout)
-    _bf16("y", y)
-    _bf16("routing weights", w)
+    dt = _half("grad_output", dout)
+    _half("y", y, dt)
+    _half("routing weights", w, dt)
     T, K = pos.shape
     H = y.shape[1]
     dy = torch.empty_like(y)
     dw = torch.empty((T, K), dtype=w.dtype, device=dev)
     _capi.call(
-        "pmx_combine_bwd", _ptr(dout), _ptr(y), _ptr(pos), _ptr(w), T, K, H, _ptr(dy), _ptr(dw), _stream(dev)
+        _sym("pmx_combine_bwd", dt), _ptr(dout), _ptr(y), _ptr(pos), _ptr(w), T, K, H, _ptr(dy), _ptr(dw),
+        _stream(dev)
     )
     return dy, dw
 
@@ -224,17 +237,17 @@ def combine_bwd_top1_rows(dout: torch.Tensor, y: torch.Tensor, row_token: torch.
     the row map of moe_scatter_src) -> (dY [T, H], dw [T, 1]); bit-identical
     to combine_bwd with the matching pos."""
     dev = _check_dev(dout, y, row_token, w)
-    _bf16("dout", dout)
-    _bf16("y", y)
-    _bf16("routing weights", w)
+    dt = _half("dout", dout)
+    _half("y", y, dt)
+    _half("routing weights", w, dt)
     T, H = dout.shape
     assert y.shape == (T, H), "top-1: one row of Y per token"
     assert row_token.dtype == torch.int32 and row_token.is_contiguous() and row_token.numel() == T
     assert w.numel() == T, "top-1 routing weights: one per token"
     dy = torch.empty((T, H), dtype=y.dtype, device=dev)
     dw = torch.empty((T, 1), dtype=w.dtype, device=dev)
-    _capi.call("pmx_combine_bwd_top1_rows", _ptr(dout), _ptr(y), _ptr(row_token), _ptr(w), T, H, _ptr(dy), _ptr(dw),
-               _stream(dev))
+    _capi.call(_sym("pmx_combine_bwd_top1_rows", dt), _ptr(dout), _ptr(y), _ptr(row_token), _ptr(w), T, H,
+               _ptr(dy), _ptr(dw), _stream(dev))
     return dy, dw
 
 
@@ -252,7 +265,7 @@ def segment_sum(source: torch.Tensor, index: torch.Tensor, num_rows: int) -> tor
     if num_rows < 0:
         raise ValueError(f"num_rows must be non-negative, got {num_rows}.")
     dev = _check_dev(source)
-    _bf16("source", source)
+    dt = _half("source", source)
     N, H = source.shape
     out = torch.empty((num_rows, H), dtype=source.dtype, device=dev)
     if num_rows == 0:
@@ -263,7 +276,8 @@ def segment_sum(source: torch.Tensor, index: torch.Tensor, num_rows: int) -> tor
     ws_bytes = _capi.load().pmx_segment_sum_workspace_bytes(N, num_rows)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     _capi.call(
-        "pmx_segment_sum", _ptr(source), _ptr(idx), N, H, num_rows, _ptr(out), _ptr(ws), ws_bytes, _stream(dev)
+        _sym("pmx_segment_sum", dt), _ptr(source), _ptr(idx), N, H, num_rows, _ptr(out), _ptr(ws), ws_bytes,
+        _stream(dev)
     )
     status = ctypes.c_int32(-1)
     _capi.call("pmx_route_status", _ptr(ws), ctypes.byref(status), _stream(dev))
@@ -281,9 +295,9 @@ def gemm_fc1_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, c
                     offsets: torch.Tensor, num_groups: int, inter: int):
     """(gu [A,2I], act [A,I]) = SwiGLU fc1 over per-copy row groups."""
     dev = _check_dev(x, w_gate, w_up, offsets)
-    _bf16("hidden", x)
-    _bf16("fc1 gate weight", w_gate)
-    _bf16("fc1 up weight", w_up)
+    dt = _half("hidden", x)
+    _half("fc1 gate weight", w_gate, dt)
+    _half("fc1 up weight", w_up, dt)
     A, H = x.shape
     G, inter, copy_stride = int(num_groups), int(inter), int(copy_stride)
     assert offsets.dtype == torch.int32 and offsets.numel() == G + 1, "offsets must be int32 [num_groups + 1]"
@@ -296,7 +310,7 @@ def gemm_fc1_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, c
     gu = torch.empty((A, 2 * inter), dtype=x.dtype, device=dev)
     act = torch.empty((A, inter), dtype=x.dtype, device=dev)
     _capi.call(
-        "pmx_gemm_fc1_swiglu_fwd", _ptr(x), _ptr(w_gate), _ptr(w_up), int(copy_stride), _ptr(offsets),
+        _sym("pmx_gemm_fc1_swiglu_fwd", dt), _ptr(x), _ptr(w_gate), _ptr(w_up), int(copy_stride), _ptr(offsets),
         int(num_groups), A, H, int(inter), _ptr(gu), _ptr(act), _stream(dev),
     )
     return gu, act
@@ -305,14 +319,14 @@ def gemm_fc1_swiglu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, c
 def group_gemm_nt(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor) -> torch.Tensor:
     """C[rows of g] = a[rows of g] @ b[g]^T, b: [G, N, K]."""
     dev = _check_dev(a, b, offsets)
-    _bf16("a", a)
-    _bf16("b", b)
+    dt = _half("a", a)
+    _half("b", b, dt)
     G, N, K = b.shape
     assert a.shape[1] == K, "a and b disagree on K"
     assert offsets.numel() == G + 1
     M = a.shape[0]
     c = torch.empty((M, N), dtype=a.dtype, device=dev)
-    _capi.call("pmx_group_gemm_nt", _ptr(a), _ptr(b), _ptr(offsets), G, M, N, K, _ptr(c), _stream(dev))
+    _capi.call(_sym("pmx_group_gemm_nt", dt), _ptr(a), _ptr(b), _ptr(offsets), G, M, N, K, _ptr(c), _stream(dev))
     return c
 
 
@@ -321,9 +335,9 @@ def group_gemm_nt_combine_top1(a: torch.Tensor, b: torch.Tensor, offsets: torch.
     """Top-1 layers: C = group_gemm_nt(a, b, offsets) and, in the same kernel,
     out[row_token[r]] = bf16(C[r] * row_weight[r]) (the combine) -> (C, out)."""
     dev = _check_dev(a, b, offsets, row_token, row_weight)
-    _bf16("a", a)
-    _bf16("b", b)
-    _bf16("row weights", row_weight)
+    dt = _half("a", a)
+    _half("b", b, dt)
+    _half("row weights", row_weight, dt)
     G, N, K = b.shape
     M = a.shape[0]
     assert a.shape[1] == K, "a and b disagree on K"
@@ -332,7 +346,7 @@ def group_gemm_nt_combine_top1(a: torch.Tensor, b: torch.Tensor, offsets: torch.
     assert row_weight.numel() == M, "top-1 routing weights: one per row"
     c = torch.empty((M, N), dtype=a.dtype, device=dev)
     out = torch.empty((M, N), dtype=a.dtype, device=dev)
-    _capi.call("pmx_group_gemm_nt_combine_top1", _ptr(a), _ptr(b), _ptr(offsets), G, M, N, K, _ptr(c),
+    _capi.call(_sym("pmx_group_gemm_nt_combine_top1", dt), _ptr(a), _ptr(b), _ptr(offsets), G, M, N, K, _ptr(c),
                _ptr(row_token), _ptr(row_weight), _ptr(out), _stream(dev))
     return c, out
 
@@ -350,12 +364,12 @@ def group_gemm_nn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor,
     """C[rows of g] = a[rows of g] @ cat(b, b_second, dim=1)[g], b: [G, K(, +K2), N];
     with ``row_token`` (top-1 layers) row r goes to row row_token[r] of C."""
     dev = _check_dev(a, b, offsets, b_second, row_token)
-    _bf16("a", a)
-    _bf16("b", b)
+    dt = _half("a", a)
+    _half("b", b, dt)
     G, K0, N = b.shape
     K = K0 + (b_second.shape[1] if b_second is not None else 0)
     if b_second is not None:
-        _bf16("b_second", b_second)
+        _half("b_second", b_second, dt)
         assert b_second.shape[0] == G and b_second.shape[2] == N and b_second.shape[1] == K0
     assert a.shape[1] == K, "a and b disagree on K"
     assert offsets.numel() == G + 1
@@ -363,10 +377,10 @@ def group_gemm_nn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor,
     c = torch.empty((M, N), dtype=a.dtype, device=dev)
     split = K0 if b_second is not None else 0
     if row_token is None:
-        _capi.call("pmx_group_gemm_nn", _ptr(a), _ptr(b), _ptr(b_second), K0 * N, split, _ptr(offsets), G, M, N, K,
-                   _ptr(c), _stream(dev))
+        _capi.call(_sym("pmx_group_gemm_nn", dt), _ptr(a), _ptr(b), _ptr(b_second), K0 * N, split, _ptr(offsets),
+                   G, M, N, K, _ptr(c), _stream(dev))
     else:
-        _capi.call("pmx_group_gemm_nn_unpermute_top1", _ptr(a), _ptr(b), _ptr(b_second), K0 * N, split,
+        _capi.call(_sym("pmx_group_gemm_nn_unpermute_top1", dt), _ptr(a), _ptr(b), _ptr(b_second), K0 * N, split,
                    _ptr(offsets), G, M, N, K, _ptr(row_token), _ptr(c), _stream(dev))
     return c
 
@@ -375,15 +389,15 @@ def gemm_fc2_dgrad_swiglu(dy: torch.Tensor, w_down: torch.Tensor, gu: torch.Tens
                           offsets: torch.Tensor) -> torch.Tensor:
     """dG1 [A,2I] = SwiGLU backward of (dy @ w_down[g]) given the saved gate/up."""
     dev = _check_dev(dy, w_down, gu, offsets)
-    _bf16("dy", dy)
-    _bf16("w_down", w_down)
-    _bf16("gu", gu)
+    dt = _half("dy", dy)
+    _half("w_down", w_down, dt)
+    _half("gu", gu, dt)
     G, H, I = w_down.shape
     A = dy.shape[0]
     assert dy.shape[1] == H and gu.shape == (A, 2 * I)
     dg1 = torch.empty((A, 2 * I), dtype=dy.dtype, device=dev)
     _capi.call(
-        "pmx_gemm_fc2_dgrad_swiglu_bwd", _ptr(dy), _ptr(w_down), _ptr(gu), _ptr(offsets), G, A, H, I,
+        _sym("pmx_gemm_fc2_dgrad_swiglu_bwd", dt), _ptr(dy), _ptr(w_down), _ptr(gu), _ptr(offsets), G, A, H, I,
         _ptr(dg1), _stream(dev),
     )
     return dg1
@@ -393,12 +407,12 @@ def weight_rows(act: torch.Tensor, row_w: torch.Tensor) -> torch.Tensor:
     """out[r] = bf16(act[r] * row_w[r]) -> [R, N]: the router weight applied
     to the fc2 input (the reference's non-EP path)."""
     dev = _check_dev(act, row_w)
-    _bf16("act", act)
-    _bf16("row weights", row_w)
+    dt = _half("act", act)
+    _half("row weights", row_w, dt)
     R, N = act.shape
     assert row_w.numel() == R and row_w.is_contiguous(), "one router weight per row"
     out = torch.empty_like(act)
-    _capi.call("pmx_weight_rows", _ptr(act), _ptr(row_w), R, N, _ptr(out), _stream(dev))
+    _capi.call(_sym("pmx_weight_rows", dt), _ptr(act), _ptr(row_w), R, N, _ptr(out), _stream(dev))
     return out
 
 
@@ -409,16 +423,17 @@ def swiglu_bwd_weighted(d_act_w: torch.Tensor, gu: torch.Tensor, act: torch.Tens
     gradient dw[row_src[r]] = bf16(sum_j bf16(act[r,j] * d_act_w[r,j]))
     -> (dG1, dw [num_assign] bf16; entries no row names are not written)."""
     dev = _check_dev(d_act_w, gu, act, row_w, row_src)
-    for name, t in (("d_act_w", d_act_w), ("gu", gu), ("act", act), ("row weights", row_w)):
-        _bf16(name, t)
+    dt = _half("act", act)
+    for name, t in (("d_act_w", d_act_w), ("gu", gu), ("row weights", row_w)):
+        _half(name, t, dt)
     R, I = act.shape
     assert d_act_w.shape == (R, I) and gu.shape == (R, 2 * I), "d_act_w [R, I], gu [R, 2I]"
     assert row_w.numel() == R and row_w.is_contiguous()
     assert row_src.dtype == torch.int32 and row_src.is_contiguous() and row_src.numel() == R
     dg1 = torch.empty((R, 2 * I), dtype=act.dtype, device=dev)
     dw = torch.empty(num_assign, dtype=row_w.dtype, device=dev)
-    _capi.call("pmx_swiglu_bwd_weighted", _ptr(d_act_w), _ptr(gu), _ptr(act), _ptr(row_w), _ptr(row_src), R, I,
-               num_assign, _ptr(dg1), _ptr(dw), _stream(dev))
+    _capi.call(_sym("pmx_swiglu_bwd_weighted", dt), _ptr(d_act_w), _ptr(gu), _ptr(act), _ptr(row_w), _ptr(row_src),
+               R, I, num_assign, _ptr(dg1), _ptr(dw), _stream(dev))
     return dg1, dw
 
 
@@ -429,8 +444,8 @@ def group_gemm_tn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, split
     [G, M - split, N] (split fc1 weight gradients).
     """
     dev = _check_dev(a, b, offsets)
-    _bf16("a", a)
-    _bf16("b", b)
+    dt = _half("a", a)
+    _half("b", b, dt)
     M, N = a.shape[1], b.shape[1]
     K = a.shape[0]
     assert b.shape[0] == K, "a and b must have the same rows"
@@ -443,15 +458,16 @@ def group_gemm_tn(a: torch.Tensor, b: torch.Tensor, offsets: torch.Tensor, split
     if split is None:
         c0 = torch.empty((G, M, N), dtype=a.dtype, device=dev)
         _capi.call(
-            "pmx_group_gemm_tn", _ptr(a), _ptr(b), _ptr(offsets), G, K, M, N, _ptr(c0), None, M * N, 0, _stream(dev)
+            _sym("pmx_group_gemm_tn", dt), _ptr(a), _ptr(b), _ptr(offsets), G, K, M, N, _ptr(c0), None, M * N,
+            0, _stream(dev)
         )
         return c0
     assert M - split == split, "split gradients must have equal halves"
     c0 = torch.empty((G, split, N), dtype=a.dtype, device=dev)
     c1 = torch.empty((G, split, N), dtype=a.dtype, device=dev)
     _capi.call(
-        "pmx_group_gemm_tn", _ptr(a), _ptr(b), _ptr(offsets), G, K, M, N, _ptr(c0), _ptr(c1), split * N, split,
-        _stream(dev),
+        _sym("pmx_group_gemm_tn", dt), _ptr(a), _ptr(b), _ptr(offsets), G, K, M, N, _ptr(c0), _ptr(c1), split * N,
+        split, _stream(dev),
     )
     return c0, c1
 
@@ -471,7 +487,7 @@ def replica_fold(grads: torch.Tensor, copy_offsets: torch.Tensor, copy_slots: to
     here reads it back, so the call never synchronises the host.
     """
     dev = _check_dev(grads, copy_offsets, copy_slots, slot_tokens, status)
-    _bf16("grads", grads)
+    dt = _half("grads", grads)
     assert copy_offsets.dtype == torch.int32 and copy_slots.dtype == torch.int32
     assert copy_offsets.numel() == int(num_experts) + 1, "copy_offsets must have num_experts + 1 entries"
     if status is not None:
@@ -483,7 +499,7 @@ def replica_fold(grads: torch.Tensor, copy_offsets: torch.Tensor, copy_slots: to
         slot_tokens = slot_tokens.to(torch.int64).contiguous()
         assert slot_tokens.numel() == C
     _capi.call(
-        "pmx_replica_fold", _ptr(grads), _ptr(copy_offsets), _ptr(copy_slots), _ptr(slot_tokens),
+        _sym("pmx_replica_fold", dt), _ptr(grads), _ptr(copy_offsets), _ptr(copy_slots), _ptr(slot_tokens),
         int(num_experts), C, P, ctypes.cast(out.data_ptr(), ctypes.POINTER(ctypes.c_float)),
         1 if writeback else 0, _ptr(status), _stream(dev),
     )

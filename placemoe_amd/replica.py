@@ -160,7 +160,7 @@ class OverlappedReplicaSync:
 # Cross-rank replica-gradient exchange: one rank's side
 # ---------------------------------------------------------------------------
 
-PMX_DTYPE = {torch.bfloat16: 0, torch.float32: 1}
+PMX_DTYPE = {torch.bfloat16: 0, torch.float32: 1, torch.float16: 2}
 
 
 @dataclass(frozen=True)

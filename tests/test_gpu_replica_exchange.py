@@ -91,7 +91,7 @@ def test_reference_known_answers(case):
 @pytest.mark.parametrize("max_ranks", [2, 3])
 @pytest.mark.parametrize("seed", [0, 1, 2, 3])
 @pytest.mark.parametrize("dtypes", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32),
-                                    (torch.bfloat16, torch.float32)])
+                                    (torch.bfloat16, torch.float32), (torch.float16, torch.float16)])
 def test_random_layouts_match_oracle(max_ranks, seed, dtypes):
     rng = np.random.default_rng(seed)
     R, nl, E = 4, 6, 11
@@ -110,10 +110,12 @@ def test_random_layouts_match_oracle(max_ranks, seed, dtypes):
             got = grads[r][p].cpu().double()
             ex = exact[r][p]
             scale = ex.abs().max().item() + 1e-30
-            if dt == torch.bfloat16:
-                # partial sums cross ranks in bf16 (the reference's buffer dtype), so a total is
-                # rounded at most twice: the sending rank's partial, then the fp32 total
-                assert (got - ex).abs().max().item() <= 2 ** -7 * ex.abs().max().item() + 1e-6
+            if dt in (torch.bfloat16, torch.float16):
+                # partial sums cross ranks in the 16-bit gradient dtype (the reference's buffer
+                # dtype), so a total is rounded at most twice: the sending rank's partial, then
+                # the fp32 total (bf16: 8 significant bits, fp16: 11)
+                ulp = 2 ** -7 if dt == torch.bfloat16 else 2 ** -10
+                assert (got - ex).abs().max().item() <= ulp * ex.abs().max().item() + 1e-6
                 assert (got - oracle[r][p].double()).abs().max().item() / scale <= 1e-2
             else:
                 assert (got - ex).abs().max().item() / scale <= 1e-6

@@ -95,8 +95,11 @@ def test_raw_forward_weight_combination_errors():
         fused_moe.hip_fused_moe_forward(1, w, sel, x, fc, fc, fc, fc1_1_2_weight=fc)
     with pytest.raises(ValueError, match="Split fc1 mode"):
         fused_moe.hip_fused_moe_forward(1, w, sel, x, fc, None, fc)
-    with pytest.raises(NotImplementedError, match="bfloat16"):
+    # bf16 or fp16, the weights in the hidden states' dtype (checked before any device work)
+    with pytest.raises(AssertionError, match="like the hidden states"):
         fused_moe.hip_fused_moe_forward(1, w, sel, x.half(), None, None, fc, fc1_1_2_weight=fc)
+    with pytest.raises(AssertionError, match="bfloat16 or float16"):
+        fused_moe.hip_fused_moe_forward(1, w, sel, x.float(), None, None, fc, fc1_1_2_weight=fc)
 
 
 def test_kernels_refuse_cpu_tensors():
