@@ -88,6 +88,7 @@ class EventTimer:
 
     @contextlib.contextmanager
     def __call__(self, name):
+        name = name[:-4] if name.endswith("_f16") else name  # fp16 twins count as their stage
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         idx = self._seen[name]
@@ -124,6 +125,9 @@ def parse():
                         "instead of in the fc2 and fc1-dgrad epilogues")
     p.add_argument("--no-backward-overlap", action="store_true",
                    help="run the backward's independent GEMM pairs one after the other on one stream")
+    p.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"],
+                   help="tensor dtype of the layer (the metric is quoted on bf16; fp16 runs the *_f16 "
+                        "entry points on the same workload cast to fp16)")
     p.add_argument("--layers", type=int, default=1,
                    help="stack this many layers (own copy weights and placement each) per step; with --config "
                         "fold, each layer's replica fold runs on a side stream beside the backward of the "
@@ -159,7 +163,7 @@ def layer_stack(wl, dev, layers: int, steps: int, warmup: int, fold: bool):
     sync = placemoe_amd.OverlappedReplicaSync(mods) if fold else None
     x = wl.hidden.detach().requires_grad_(True)
     w = wl.routing_weights.detach()
-    dout = torch.randn_like(wl.hidden, dtype=torch.float32).to(torch.bfloat16)
+    dout = torch.randn_like(wl.hidden, dtype=torch.float32).to(wl.hidden.dtype)
 
     def step():
         h = x
@@ -528,6 +532,10 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     wl = make_workload(args.config, device=dev)
+    dt = torch.float16 if args.dtype == "fp16" else torch.bfloat16
+    if dt != torch.bfloat16:
+        for f in ("hidden", "routing_weights", "fc1", "fc2"):
+            setattr(wl, f, getattr(wl, f).to(dt))
     backward = not wl.meta.get("forward_only", False)
     T, K, H, I, C = wl.T, wl.K, wl.H, wl.I, wl.C
     work = algorithmic_work(T, K, H, I, C)
@@ -535,14 +543,14 @@ def main():
     w = wl.routing_weights.requires_grad_(backward)
     fc1 = wl.fc1.requires_grad_(backward)
     fc2 = wl.fc2.requires_grad_(backward)
-    dout = torch.randn((T, H), device=dev, generator=torch.Generator(device=dev).manual_seed(1)).to(torch.bfloat16)
+    dout = torch.randn((T, H), device=dev, generator=torch.Generator(device=dev).manual_seed(1)).to(dt)
 
     fold = args.config == "fold"
     if args.layers > 1:
         ms = layer_stack(wl, dev, args.layers, args.steps, args.warmup, fold)
         print(json.dumps({"metric": "MoE layer fwd+bwd ms", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
-                          "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+                          "higher_is_better": False, "dtype": args.dtype, "data": "synthetic",
                           "config": {"workload": args.config, "layers": args.layers,
                                      "replica_fold": "overlapped per layer" if fold else None}}), flush=True)
         return 0
@@ -630,7 +638,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": "synthetic",
         "config": {"workload": f"config{['toy', 'qwen3', 'dsv3', 'skew', 'fold'].index(args.config) + 1}-"
                                f"{args.config}", "tokens": T, "top_k": K, "hidden": H, "moe_intermediate": I,
