@@ -8,6 +8,8 @@
 * oracle_small.npz - small vectors produced by oracle/moe_oracle.py for a fixed
   seed (routing, layer forward and backward), re-checked by the CPU suite so a
   change in the oracle cannot pass silently, and used by the GPU suite.
+* oracle_small_f16.npz - the same draws cast to fp16 instead of bf16, with the
+  oracle's fp16 outputs.
 
 Usage: python tests/golden/make_golden.py
 """
@@ -55,7 +57,7 @@ KATS = {
 }
 
 
-def small_vectors():
+def small_vectors(dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(424242)
     T, K, H, I, E, S = 48, 3, 64, 32, 5, 3
     L = np.array([0, 1, 2, 3, 4, 0, 2, 2], dtype=np.int64)
@@ -63,15 +65,15 @@ def small_vectors():
     M = np.array([[0, 1, 2, 3, 4], [5, 1, 6, 3, 4], [0, 1, 7, 3, 4]], dtype=np.int64)
     src = torch.randint(0, S, (T,), generator=g).numpy()
     sel = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).numpy()
-    x = torch.randn((T, H), generator=g).to(torch.bfloat16)
-    w = torch.rand((T, K), generator=g).to(torch.bfloat16)
-    w1 = (torch.randn((C, 2 * I, H), generator=g) * 0.1).to(torch.bfloat16)
-    w2 = (torch.randn((C, H, I), generator=g) * 0.1).to(torch.bfloat16)
-    dout = torch.randn((T, H), generator=g).to(torch.bfloat16)
+    x = torch.randn((T, H), generator=g).to(dtype)
+    w = torch.rand((T, K), generator=g).to(dtype)
+    w1 = (torch.randn((C, 2 * I, H), generator=g) * 0.1).to(dtype)
+    w2 = (torch.randn((C, H, I), generator=g) * 0.1).to(dtype)
+    dout = torch.randn((T, H), generator=g).to(dtype)
     phys, counts, offsets, pos = O.route(M, src, sel, C)
     fwd = O.moe_layer_forward(x, w, phys, w1, w2)
     bwd = O.moe_layer_backward(dout, fwd, w, w1, w2)
-    f32 = lambda t: t.float().numpy()  # noqa: E731  bf16 values are exact in fp32
+    f32 = lambda t: t.float().numpy()  # noqa: E731  bf16 and fp16 values are exact in fp32
     return dict(
         slot_to_logical=L, mapping=M, sources=src, selected=sel, hidden=f32(x), routing_weights=f32(w),
         fc1=f32(w1), fc2=f32(w2), grad_out=f32(dout), phys=phys, counts=counts, offsets=offsets, pos=pos,
@@ -84,6 +86,7 @@ def main():
     with open(os.path.join(HERE, "reference_kats.json"), "w") as f:
         json.dump(KATS, f, indent=1)
     np.savez_compressed(os.path.join(HERE, "oracle_small.npz"), **small_vectors())
+    np.savez_compressed(os.path.join(HERE, "oracle_small_f16.npz"), **small_vectors(torch.float16))
     print("wrote", HERE)
 
 

@@ -20,8 +20,8 @@ def kats():
         return json.load(f)
 
 
-def small():
-    return dict(np.load(os.path.join(GOLDEN, "oracle_small.npz")))
+def small(name="oracle_small.npz"):
+    return dict(np.load(os.path.join(GOLDEN, name)))
 
 
 def test_source_lut_kat():
@@ -64,9 +64,11 @@ def test_replica_sum_kat():
     assert torch.all(O.replica_fold(down.to(torch.bfloat16), L, 4)[e] == k["expected_down"])
 
 
-def test_oracle_reproduces_recorded_vectors():
-    v = small()
-    bf = lambda a: torch.as_tensor(a).to(torch.bfloat16)  # noqa: E731
+@pytest.mark.parametrize("name,dtype", [("oracle_small.npz", torch.bfloat16),
+                                        ("oracle_small_f16.npz", torch.float16)])
+def test_oracle_reproduces_recorded_vectors(name, dtype):
+    v = small(name)
+    bf = lambda a: torch.as_tensor(a).to(dtype)  # noqa: E731
     phys, counts, offsets, pos = O.route(v["mapping"], v["sources"], v["selected"], v["slot_to_logical"].size)
     for name, got in (("phys", phys), ("counts", counts), ("offsets", offsets), ("pos", pos)):
         assert np.array_equal(got, v[name]), name
